@@ -1,0 +1,201 @@
+"""Benchmark: ms per SpMM and achieved HBM GB/s of the fused INT8-dequant SpMM on one MI355X.
+
+Workload (BASELINE.json configs[2] / [3]): the synthetic 2,449,029-row / 126,167,053-nnz power-law
+matrix ("c3"), F128 (the line's `value`) and F256 (reported under "f256"). A "step" is one
+launchSpmmInt8 over the whole matrix with A, X, scales and the workspace already resident in HBM.
+Timing mirrors the reference harness (src/main.cu:30-51): W warm-up launches, synchronize, then
+HIP events (on the launch stream) around K launches; ms_per_step = elapsed / K.
+
+Roofline: algorithmic bytes per launch B_alg = B_A + B_X + B_Y + B_P, computed from the format:
+  B_A = 4 nnz + 12 S + 4 P + 68 nSW + 28 T + 32 nSplitSW + 4 K   (A stream, read once)
+  B_X = (F + 4) U                                                (each referenced X row + scale once)
+  B_Y = 4 R F                                                    (Y written once)
+  B_P = 64 F K                                                   (partial tiles written + read once)
+achieved = B_alg / kernel time, peak = 8.0e12 B/s. `traffic` (measured HBM bytes per launch) is read
+from profiles/counters_<workload>.json when a counter profile of this workload is present.
+
+cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over a bounded prefix of
+SWs (~10 s of CPU work), extrapolated by SW count to one full SpMM.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12
+METRIC = "ms/SpMM + achieved HBM GB/s, 2.45M-row 126M-nnz power-law A, F128/F256"
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(fmt, csr_sources: np.ndarray, features: int) -> dict:
+    s = fmt.sizes()
+    tasks = fmt.arrays(copy=False)["tasks"]
+    n_split = int(s.reductions // 4)
+    distinct = int(np.unique(csr_sources).size)
+    b_a = (4 * s.values + 12 * s.sourceIds + 4 * s.rowGroupMasks + 68 * (s.windowOffsets - 1)
+           + 28 * s.tasks + 32 * n_split + 4 * s.partialCount)
+    b_x = (features + 4) * distinct
+    b_y = 4 * s.rows * features
+    b_p = 64 * features * s.partialCount
+    return {"B_A": int(b_a), "B_X": int(b_x), "B_Y": int(b_y), "B_P": int(b_p),
+            "B_alg": int(b_a + b_x + b_y + b_p), "distinct_sources": distinct,
+            "split_tasks": int(np.count_nonzero(tasks["partial"] != 0xFFFFFFFF))}
+
+
+def time_launches(dm, packed, scale, y, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        dm.spmm(packed, scale, y, stream=stream)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        dm.spmm(packed, scale, y, stream=stream)
+    end.record(stream)
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def run_workload(csr, fmt, features, seed, steps, warmup, dev):
+    import torch
+    import tcc_spmm_amd as T
+    from tcc_spmm_amd.device import TorchDeviceMatrix, pack_features_int8x16, quantize_features_int8
+
+    t0 = time.time()
+    x = T.synth_features(csr.cols, features, seed)
+    xq, scale = quantize_features_int8(torch.from_numpy(x).to(dev))
+    del x
+    packed = pack_features_int8x16(xq)
+    del xq
+    dm = TorchDeviceMatrix(fmt, features, device=dev)
+    y = torch.empty((csr.rows, features), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    log(f"F{features}: X prepared and format uploaded in {time.time() - t0:.1f}s")
+    stream = torch.cuda.Stream()
+    # Reference-style protocol, repeated 5 times: report the median of the 5 means.
+    means = [time_launches(dm, packed, scale, y, steps, warmup if i == 0 else 2, stream)
+             for i in range(5)]
+    ms = float(np.median(means))
+    assert int(dm.counters.abs().sum()) == 0 if dm.counters is not None else True
+    y0 = y[0, :8].cpu().numpy().tolist()
+    del dm, y, packed, scale
+    torch.cuda.empty_cache()
+    return ms, means, y0
+
+
+def cpu_baseline(csr, fmt, features, seed, budget_s=10.0):
+    """Oracle FP32 SpMM on the host over a bounded SW prefix, extrapolated to one full SpMM."""
+    import tcc_spmm_amd as T
+    from oracle import Oracle
+    orc = Oracle()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    views = csr.views()
+    of = orc.sw32(csr.rows, csr.cols, *views)
+    n_sw = len(fmt.window_offsets) - 1
+    x = T.synth_features(csr.cols, features, seed)
+    q, sc = orc.quantize(x)
+    del x
+    packed = orc.pack16(q)
+    del q
+    y = np.zeros((csr.rows, features), np.float32)
+    probe = min(n_sw, 2000)
+    t = time.time()
+    of.spmm_f32_mt(packed, sc, 0, probe, threads, y)
+    dt = time.time() - t
+    sample = min(n_sw, max(probe, int(probe * budget_s / max(dt, 1e-3))))
+    t = time.time()
+    _, used = of.spmm_f32_mt(packed, sc, 0, sample, threads, y)
+    dt = time.time() - t
+    wo = fmt.window_offsets
+    frac_panels = float(wo[sample] - wo[0]) / float(wo[-1] - wo[0])
+    ms_full = dt * 1e3 / frac_panels
+    return {"value": round(ms_full, 3), "unit": "ms/SpMM", "cores": int(used), "kind": "port",
+            "sample": f"first {sample} of {n_sw} SWs ({frac_panels:.1%} of panels), FP32 TF32-operand "
+                      f"SpMM from oracle/tcc_oracle.c, {dt:.1f}s measured, scaled by panel share"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-f256", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
+              "design); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tcc_spmm_amd as T
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    dev = torch.device("cuda:0")
+
+    t0 = time.time()
+    csr = T.synth_csr(args.config)
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    stats = fmt.stats()
+    log(f"{args.config}: generated + converted in {time.time() - t0:.1f}s: {stats}")
+    src = csr.views()[1]
+
+    results = {}
+    for feats, seed in ((128, 103), (256, 104)):
+        if feats == 256 and args.no_f256:
+            continue
+        ms, means, y0 = run_workload(csr, fmt, feats, seed, args.steps, args.warmup, dev)
+        b = algorithmic_bytes(fmt, src, feats)
+        achieved = b["B_alg"] / (ms * 1e-3)
+        traffic = None
+        prof = ROOT / "profiles" / f"counters_{args.config}_f{feats}.json"
+        if prof.exists():
+            traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
+        results[feats] = {
+            "ms": round(ms, 4), "means_ms": [round(m, 4) for m in means],
+            "gbps": round(achieved / 1e9, 1), "bytes": b, "y00_07": y0,
+            "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1),
+                         "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic},
+        }
+        log(f"F{feats}: {ms:.4f} ms/SpMM, {achieved / 1e9:.1f} GB/s algorithmic "
+            f"({achieved / HBM_PEAK:.1%} of 8 TB/s), runs {means}")
+
+    base = None
+    if not args.no_cpu_baseline:
+        t = time.time()
+        base = cpu_baseline(csr, fmt, 128, 103)
+        log(f"cpu baseline: {base} ({time.time() - t:.1f}s)")
+
+    r = results[128]
+    line = {
+        "metric": METRIC, "value": r["ms"], "unit": "ms/SpMM", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["ms"], "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8->tf32xfp32", "data": "synthetic",
+        "config": {"workload": f"{args.config}: {stats['rows']}x{stats['cols']}, nnz={stats['nnz']}, "
+                               f"F128 (f256 below)", "features": 128, "sw": stats["sw"],
+                   "tasks": stats["tasks"], "split_sw": stats["split_sw"],
+                   "partial_count": stats["partial_count"], "panels": stats["panels"]},
+        "gbps": r["gbps"], "roofline": r["roofline"], "cpu_baseline": base,
+        "f256": results.get(256), "f128_detail": {k: r[k] for k in ("means_ms", "bytes", "y00_07")},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

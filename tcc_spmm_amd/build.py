@@ -1,0 +1,82 @@
+"""Build libtcc_spmm.so in-tree for gfx950.
+
+HIP sources (*.hip) go through hipcc for gfx950 with packed-FP32 instructions disabled; host-only
+C++ sources (*.cpp) go through g++ against the ROCm headers. Objects land in tcc_spmm_amd/_build/,
+the library in tcc_spmm_amd/libtcc_spmm.so. Run ``python -m tcc_spmm_amd.build``.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import pathlib
+import shlex
+import subprocess
+import sys
+
+PKG = pathlib.Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libtcc_spmm.so"
+ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = os.environ.get("TCC_OFFLOAD_ARCH", "gfx950")
+
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+]
+CXX_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "-pthread", "-D__HIP_PLATFORM_AMD__",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}", f"-I{ROCM / 'include'}",
+]
+
+
+def _sources():
+    return sorted(p for p in CSRC.rglob("*") if p.suffix in (".hip", ".cpp"))
+
+
+def _compile(src: pathlib.Path) -> pathlib.Path:
+    rel = src.relative_to(CSRC)
+    obj = BUILD / (str(rel).replace(os.sep, "__") + ".o")
+    if src.suffix == ".hip":
+        cmd = [str(ROCM / "bin" / "hipcc"), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [os.environ.get("CXX", "g++"), *CXX_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {shlex.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    BUILD.mkdir(exist_ok=True)
+    srcs = _sources()
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        objs = list(pool.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [str(ROCM / "bin" / "hipcc"), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp),
+           *map(str, objs), "-lpthread"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {shlex.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+def build_oracle(verbose: bool = False) -> None:
+    """Compile oracle/ (C restatement, and the reference's own CPU format code when present)."""
+    res = subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{res.stdout}\n{res.stderr}")
+    if verbose:
+        print("built oracle")
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    if "--with-oracle" in sys.argv:
+        build_oracle(verbose=True)

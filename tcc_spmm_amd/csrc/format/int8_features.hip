@@ -1,0 +1,100 @@
+// Per-source INT8 quantization and packed16 byte permutation for gfx950 (wave64).
+//
+// quantize: one wave per source row (4 rows per 256-thread workgroup). Lanes stride the row with
+// coalesced loads, the row's |x| maximum is reduced across the wave with DPP-backed shuffles, and
+// every element is divided by the scale with the IEEE-correct FP32 divide and rounded half-to-even.
+// Results are bit-identical to reference src/format/int8_quantize.cu:4-25.
+//
+// pack: one thread per 16-byte tile; four v_perm_b32 byte shuffles turn q[0..15] into
+// [q0,q8,q1,q9,...,q7,q15] (reference src/format/pack_int8.cu:6-15). Unaligned buffers use a
+// byte-pair kernel with the same result.
+#include "format/int8_features.h"
+#include "hip_support.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <stdexcept>
+
+namespace {
+
+constexpr unsigned kWave = 64;
+constexpr unsigned kRowsPerBlock = 4;
+
+__global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
+    const float* __restrict__ x, std::int8_t* __restrict__ q, float* __restrict__ scale,
+    unsigned sources, unsigned features) {
+    const unsigned lane = threadIdx.x & (kWave - 1);
+    const unsigned row = blockIdx.x * kRowsPerBlock + (threadIdx.x / kWave);
+    if (row >= sources) return;
+    const float* xr = x + std::size_t(row) * features;
+    float m = 0.0f;
+    for (unsigned j = lane; j < features; j += kWave) m = fmaxf(m, fabsf(xr[j]));
+#pragma unroll
+    for (unsigned offset = kWave / 2; offset > 0; offset >>= 1) m = fmaxf(m, __shfl_xor(m, offset));
+    const float s = m == 0.0f ? 1.0f : m / 127.0f;
+    if (lane == 0) scale[row] = s;
+    std::int8_t* qr = q + std::size_t(row) * features;
+    for (unsigned j = lane; j < features; j += kWave) {
+        const int v = __float2int_rn(xr[j] / s);
+        qr[j] = std::int8_t(v < -127 ? -127 : (v > 127 ? 127 : v));
+    }
+}
+
+__global__ __launch_bounds__(256) void packTiles(const uint4* __restrict__ q,
+                                                 uint4* __restrict__ out, std::size_t tiles) {
+    const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= tiles) return;
+    const uint4 w = q[t];
+    // v_perm_b32 selectors: bytes 0-3 pick from the second operand, 4-7 from the first.
+    uint4 r;
+    r.x = __builtin_amdgcn_perm(w.z, w.x, 0x05010400u); // q0  q8  q1  q9
+    r.y = __builtin_amdgcn_perm(w.z, w.x, 0x07030602u); // q2  q10 q3  q11
+    r.z = __builtin_amdgcn_perm(w.w, w.y, 0x05010400u); // q4  q12 q5  q13
+    r.w = __builtin_amdgcn_perm(w.w, w.y, 0x07030602u); // q6  q14 q7  q15
+    out[t] = r;
+}
+
+__global__ __launch_bounds__(256) void packPairs(const std::uint8_t* __restrict__ q,
+                                                 unsigned short* __restrict__ out,
+                                                 std::size_t pairs) {
+    const std::size_t p = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= pairs) return;
+    const std::size_t o = (p >> 3) * 16 + (p & 7);
+    out[p] = static_cast<unsigned short>(q[o] | (unsigned(q[o + 8]) << 8));
+}
+
+} // namespace
+
+void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uint32_t sources,
+                          std::uint32_t features, hipStream_t stream) {
+    // A zero-sized grid is a launch error, reported like the runtime would (std::runtime_error).
+    if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
+    const unsigned blocks = (sources + kRowsPerBlock - 1) / kRowsPerBlock;
+    hipLaunchKernelGGL(quantizeRows, dim3(blocks), dim3(kWave * kRowsPerBlock), 0, stream, x, q,
+                       scale, sources, features);
+    checkHip(hipGetLastError());
+}
+
+void packFeaturesInt8x16(const std::int8_t* q, std::int8_t* packed, std::uint32_t sources,
+                         std::uint32_t features, hipStream_t stream) {
+    if (!sources || !features) throw std::runtime_error("pack: invalid configuration argument");
+    if (features % 16) throw std::invalid_argument("packed16 needs features % 16 == 0");
+    const std::size_t bytes = std::size_t(sources) * features;
+    const bool aligned = (reinterpret_cast<std::uintptr_t>(q) % 16 == 0) &&
+                         (reinterpret_cast<std::uintptr_t>(packed) % 16 == 0);
+    if (aligned) {
+        const std::size_t tiles = bytes / 16;
+        const std::size_t blocks = (tiles + 255) / 256;
+        hipLaunchKernelGGL(packTiles, dim3(unsigned(blocks)), dim3(256), 0, stream,
+                           reinterpret_cast<const uint4*>(q), reinterpret_cast<uint4*>(packed),
+                           tiles);
+    } else {
+        const std::size_t pairs = bytes / 2;
+        const std::size_t blocks = (pairs + 255) / 256;
+        hipLaunchKernelGGL(packPairs, dim3(unsigned(blocks)), dim3(256), 0, stream,
+                           reinterpret_cast<const std::uint8_t*>(q),
+                           reinterpret_cast<unsigned short*>(packed), pairs);
+    }
+    checkHip(hipGetLastError());
+}

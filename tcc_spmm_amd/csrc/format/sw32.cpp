@@ -1,0 +1,235 @@
+// SW32 host format builder and panel-task planner.
+//
+// Output contract: byte-identical arrays to the reference's convertCsrToSw32 / buildPanelTasks
+// (src/format/sw32.cpp:25-167) for the same canonical CSR — the device kernel and every
+// descriptor consumer depend on that layout. The construction is our own: instead of a
+// single-threaded 32-way heap merge, each SW sorts its (source, row) keys, and SW blocks are built
+// in parallel into private buffers that are stitched together with offset fix-ups afterwards.
+#include "format/sw32.h"
+#include "../parallel.h"
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+
+namespace {
+
+constexpr std::uint32_t kPad = std::numeric_limits<std::uint32_t>::max();
+
+std::uint32_t fit32(std::uint64_t n) {
+    if (n > std::numeric_limits<std::uint32_t>::max())
+        throw std::overflow_error("source-mask format exceeds uint32 offsets");
+    return static_cast<std::uint32_t>(n);
+}
+
+// 4-bit mask of the 8-row groups touched by a 32-bit row mask.
+inline unsigned groupsOf(std::uint32_t rowMask) {
+    unsigned g = 0;
+    for (unsigned rw = 0; rw < 4; ++rw)
+        g |= unsigned((rowMask >> (8 * rw)) & 0xFFu ? 1u : 0u) << rw;
+    return g;
+}
+
+// One block of consecutive SWs, with block-local panel and value numbering.
+struct WindowBlock {
+    std::vector<std::uint32_t> sourceIds, rowGroupMasks, bucketOffsets, windowEnds;
+    std::vector<std::uint64_t> metadata; // value base is block-local here
+    std::vector<float> values;
+};
+
+struct Entry {
+    std::uint64_t key; // source << 5 | local row
+    std::uint32_t pos; // index into the CSR arrays
+};
+
+struct Item {
+    std::uint32_t source, mask, first; // first = index of its first Entry in the sorted list
+};
+
+void buildBlock(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr, bool bucketed,
+                std::uint32_t swBegin, std::uint32_t swEnd, WindowBlock& out) {
+    std::vector<Entry> entries;
+    std::array<std::vector<Item>, 16> buckets;
+    for (std::uint32_t sw = swBegin; sw < swEnd; ++sw) {
+        const std::uint64_t base = std::uint64_t(sw) * 32;
+        const std::uint32_t count = std::uint32_t(std::min<std::uint64_t>(32, rows - base));
+        entries.clear();
+        for (std::uint32_t r = 0; r < count; ++r) {
+            const std::size_t row = base + r;
+            const std::uint32_t e0 = csr.rowOffsets[row], e1 = csr.rowOffsets[row + 1];
+            for (std::uint32_t e = e0; e < e1; ++e) {
+                const std::uint32_t s = csr.sourceIds[e];
+                const float v = csr.values[e];
+                if (s >= cols)
+                    throw std::invalid_argument("source-mask source outside column range");
+                if (!std::isfinite(v) || v == 0)
+                    throw std::invalid_argument("source-mask requires finite nonzero values");
+                if (e > e0 && s <= csr.sourceIds[e - 1])
+                    throw std::invalid_argument("source-mask requires increasing row sources");
+                entries.push_back({(std::uint64_t(s) << 5) | r, e});
+            }
+        }
+        std::sort(entries.begin(), entries.end(),
+                  [](const Entry& a, const Entry& b) { return a.key < b.key; });
+        for (auto& b : buckets) b.clear();
+        for (std::size_t i = 0; i < entries.size();) {
+            const std::uint32_t source = std::uint32_t(entries[i].key >> 5);
+            Item item{source, 0, std::uint32_t(i)};
+            while (i < entries.size() && std::uint32_t(entries[i].key >> 5) == source)
+                item.mask |= 1u << (entries[i++].key & 31);
+            buckets[bucketed ? groupsOf(item.mask) : 0].push_back(item);
+        }
+        for (unsigned slot = 0; slot < 16; ++slot) {
+            const auto& bucket = buckets[sw32BucketOrder[slot]];
+            if (bucketed) out.bucketOffsets.push_back(std::uint32_t(out.rowGroupMasks.size()));
+            unsigned inPanel = 0, panelMask = 0;
+            for (const Item& item : bucket) {
+                out.sourceIds.push_back(item.source);
+                out.metadata.push_back((std::uint64_t(out.values.size()) << 32) | item.mask);
+                const unsigned n = unsigned(__builtin_popcount(item.mask));
+                for (unsigned k = 0; k < n; ++k)
+                    out.values.push_back(csr.values[entries[item.first + k].pos]);
+                panelMask |= groupsOf(item.mask);
+                if (++inPanel == 8) {
+                    out.rowGroupMasks.push_back(panelMask);
+                    inPanel = panelMask = 0;
+                }
+            }
+            if (inPanel) {
+                for (; inPanel < 8; ++inPanel) {
+                    out.sourceIds.push_back(kPad);
+                    out.metadata.push_back(0);
+                }
+                out.rowGroupMasks.push_back(panelMask);
+            }
+        }
+        if (bucketed) out.bucketOffsets.push_back(std::uint32_t(out.rowGroupMasks.size()));
+        out.windowEnds.push_back(std::uint32_t(out.rowGroupMasks.size()));
+    }
+}
+
+} // namespace
+
+void buildPanelTasks(Sw32HostFormat& format) {
+    if (format.windowOffsets.empty())
+        throw std::invalid_argument("SW32 format has no window offsets");
+    const std::uint32_t windows = fit32(format.windowOffsets.size() - 1);
+    if (format.bucketOffsets.size() != std::size_t(windows) * 17)
+        throw std::invalid_argument("panel tasks need the RW-bucketed SW32 format");
+    format.tasks.clear();
+    format.reductions.clear();
+    format.partialIds.clear();
+    format.tasks.reserve(windows);
+    std::array<std::vector<std::uint32_t>, 4> groupTiles;
+    std::uint64_t tiles = 0;
+    for (std::uint32_t sw = 0; sw < windows; ++sw) {
+        const std::uint32_t first = format.windowOffsets[sw], last = format.windowOffsets[sw + 1];
+        const std::uint32_t panels = last - first;
+        if (panels <= sw32TaskPanelLimit) {
+            format.tasks.push_back({sw, first, last, kPad, 15, 1, 0});
+            continue;
+        }
+        const std::uint32_t chunks = (panels + sw32TaskPanelLimit - 1) / sw32TaskPanelLimit;
+        const std::uint32_t reduceFirst = fit32(format.reductions.size());
+        for (auto& g : groupTiles) g.clear();
+        const std::uint32_t* slotBounds = format.bucketOffsets.data() + std::size_t(sw) * 17;
+        for (std::uint32_t c = 0; c < chunks; ++c) {
+            const std::uint32_t begin = first + c * sw32TaskPanelLimit;
+            const std::uint32_t end = std::min(last, begin + sw32TaskPanelLimit);
+            // Row groups of every bucket (slots 1..15) overlapping this chunk.
+            std::uint32_t mask = 0;
+            for (unsigned slot = 1; slot < 16; ++slot) {
+                const std::uint32_t lo = slotBounds[slot], hi = slotBounds[slot + 1];
+                if (std::max(begin, lo) < std::min(end, hi)) mask |= sw32BucketOrder[slot];
+            }
+            format.tasks.push_back({sw, begin, end, fit32(tiles), mask, chunks, reduceFirst});
+            for (unsigned rw = 0; rw < 4; ++rw)
+                if (mask >> rw & 1u) groupTiles[rw].push_back(fit32(tiles++));
+        }
+        for (const auto& g : groupTiles) {
+            const std::uint32_t begin = fit32(format.partialIds.size());
+            format.partialIds.insert(format.partialIds.end(), g.begin(), g.end());
+            format.reductions.push_back({begin, fit32(format.partialIds.size())});
+        }
+    }
+    fit32(format.tasks.size());
+    fit32(format.reductions.size());
+    format.partialCount = fit32(tiles);
+}
+
+Sw32HostFormat convertCsrToSw32(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr,
+                                bool bucketByRwMask) {
+    if (!rows || !cols || csr.rowOffsets.size() != std::size_t(rows) + 1 ||
+        csr.rowOffsets.front() != 0 || csr.rowOffsets.back() != csr.sourceIds.size() ||
+        csr.values.size() != csr.sourceIds.size())
+        throw std::invalid_argument("invalid canonical CSR for source-mask SW32");
+    for (std::uint32_t r = 0; r < rows; ++r)
+        if (csr.rowOffsets[r] > csr.rowOffsets[r + 1])
+            throw std::invalid_argument("decreasing CSR offsets");
+
+    const std::uint32_t windows = std::uint32_t((std::uint64_t(rows) + 31) / 32);
+    // Blocks of consecutive SWs balanced by entry count, so power-law rows do not serialise.
+    const std::size_t target = std::max<std::size_t>(1, std::min<std::size_t>(windows, 4096));
+    std::vector<std::uint32_t> cut{0};
+    {
+        const std::uint64_t total = csr.sourceIds.size();
+        std::uint64_t next = total / target;
+        for (std::uint32_t w = 1; w < windows; ++w) {
+            const std::uint64_t at = csr.rowOffsets[std::size_t(w) * 32];
+            if (at >= next || w - cut.back() >= 65536) {
+                cut.push_back(w);
+                next = at + std::max<std::uint64_t>(1, total / target);
+            }
+        }
+        cut.push_back(windows);
+    }
+    const std::size_t blocks = cut.size() - 1;
+    std::vector<WindowBlock> parts(blocks);
+    tcc::parallelChunks(blocks, blocks, [&](std::size_t b, std::size_t, std::size_t) {
+        buildBlock(rows, cols, csr, bucketByRwMask, cut[b], cut[b + 1], parts[b]);
+    });
+
+    std::vector<std::uint64_t> slotAt(blocks + 1, 0), panelAt(blocks + 1, 0), valueAt(blocks + 1, 0);
+    for (std::size_t b = 0; b < blocks; ++b) {
+        slotAt[b + 1] = slotAt[b] + parts[b].sourceIds.size();
+        panelAt[b + 1] = panelAt[b] + parts[b].rowGroupMasks.size();
+        valueAt[b + 1] = valueAt[b] + parts[b].values.size();
+    }
+    fit32(panelAt[blocks]);
+    fit32(valueAt[blocks]);
+
+    Sw32HostFormat out;
+    out.rows = rows;
+    out.cols = cols;
+    out.windowOffsets.assign(std::size_t(windows) + 1, 0);
+    out.sourceIds.resize(slotAt[blocks]);
+    out.sourceMetadata.resize(slotAt[blocks]);
+    out.rowGroupMasks.resize(panelAt[blocks]);
+    out.values.resize(valueAt[blocks]);
+    if (bucketByRwMask) out.bucketOffsets.resize(std::size_t(windows) * 17);
+    tcc::parallelChunks(blocks, blocks, [&](std::size_t b, std::size_t, std::size_t) {
+        const WindowBlock& p = parts[b];
+        const std::uint32_t panel0 = std::uint32_t(panelAt[b]);
+        const std::uint64_t value0 = valueAt[b];
+        std::memcpy(out.sourceIds.data() + slotAt[b], p.sourceIds.data(), p.sourceIds.size() * 4);
+        for (std::size_t i = 0; i < p.metadata.size(); ++i) {
+            const std::uint64_t m = p.metadata[i];
+            // Padding slots keep metadata 0; real slots get the global value base.
+            out.sourceMetadata[slotAt[b] + i] =
+                p.sourceIds[i] == kPad ? m : m + (value0 << 32);
+        }
+        std::memcpy(out.rowGroupMasks.data() + panelAt[b], p.rowGroupMasks.data(),
+                    p.rowGroupMasks.size() * 4);
+        std::memcpy(out.values.data() + value0, p.values.data(), p.values.size() * 4);
+        for (std::size_t i = 0; i < p.windowEnds.size(); ++i)
+            out.windowOffsets[cut[b] + 1 + i] = p.windowEnds[i] + panel0;
+        for (std::size_t i = 0; i < p.bucketOffsets.size(); ++i)
+            out.bucketOffsets[std::size_t(cut[b]) * 17 + i] = p.bucketOffsets[i] + panel0;
+    });
+    parts.clear();
+    if (bucketByRwMask) buildPanelTasks(out);
+    return out;
+}

@@ -1,0 +1,153 @@
+"""Device-side API on torch tensors (Python mirror of include/spmm.h and
+include/format/int8_features.h).
+
+PyTorch only provides device memory and the stream; every computation runs in the HIP kernels of
+libtcc_spmm.so, reached through its C ABI. There is no fallback path: if the library or a GPU is
+missing the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ._lib import DeviceView, check, lib
+from .format import Sw32HostFormat
+
+
+def _stream_ptr(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream)
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _require_cuda(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("device entry points take CUDA (HIP) tensors")
+
+
+def quantize_features_int8(x: torch.Tensor, q: torch.Tensor | None = None,
+                           scale: torch.Tensor | None = None, stream=None):
+    """quantizeFeaturesInt8 (reference include/format/int8_features.cuh:9-10).
+
+    x: float32 [sources, features] on the GPU. Returns (q int8 [sources, features], scale f32).
+    """
+    _require_cuda(x)
+    if x.dtype != torch.float32 or x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 [sources, features] tensor")
+    sources, features = x.shape
+    q = torch.empty((sources, features), dtype=torch.int8, device=x.device) if q is None else q
+    scale = torch.empty(sources, dtype=torch.float32, device=x.device) if scale is None else scale
+    check(lib().tcc_quantize_features_int8(_ptr(x), _ptr(q), _ptr(scale), sources, features,
+                                           _stream_ptr(stream)))
+    return q, scale
+
+
+def pack_features_int8x16(q: torch.Tensor, packed: torch.Tensor | None = None, stream=None):
+    """packFeaturesInt8x16 (reference include/format/int8_features.cuh:14-15)."""
+    _require_cuda(q)
+    if q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous int8 [sources, features] tensor")
+    sources, features = q.shape
+    packed = torch.empty_like(q) if packed is None else packed
+    check(lib().tcc_pack_features_int8x16(_ptr(q), _ptr(packed), sources, features,
+                                          _stream_ptr(stream)))
+    return packed
+
+
+@dataclass
+class SpmmWorkspace:
+    """SpmmWorkspace{partials, counters} (reference include/spmm.cuh:10-13) as torch tensors."""
+
+    partials: torch.Tensor | None
+    counters: torch.Tensor | None
+
+
+def launch_spmm_int8(view: DeviceView, packed_x: torch.Tensor, scales: torch.Tensor,
+                     output: torch.Tensor, rows: int, cols: int, features: int,
+                     workspace: SpmmWorkspace | None = None, stream=None) -> None:
+    """launchSpmmInt8 (reference include/spmm.cuh:21-23): asynchronous on `stream`."""
+    _require_cuda(packed_x, scales, output)
+    ws = workspace or SpmmWorkspace(None, None)
+    check(lib().tcc_launch_spmm_int8(C.byref(view), _ptr(packed_x), _ptr(scales), _ptr(output),
+                                     rows, cols, features, _ptr(ws.partials), _ptr(ws.counters),
+                                     _stream_ptr(stream)))
+
+
+class TorchDeviceMatrix:
+    """Uploads every array of a bucketed Sw32HostFormat into torch tensors and builds the view.
+
+    The workspace is allocated like the reference's DeviceMatrix (src/device_matrix.cuh:21-27):
+    partials = partialCount * 8 * features floats, counters = nSW * features/128 zeroed uint32,
+    both only when the plan has split SWs. Tests may poison or inspect them.
+    """
+
+    def __init__(self, fmt: Sw32HostFormat, features: int, device="cuda"):
+        if not fmt.bucketed:
+            raise ValueError("launchSpmmInt8 needs the RW-bucketed SW32 format")
+        arrs = fmt.arrays(copy=False)
+        self.rows, self.cols = fmt.rows, fmt.cols
+        self.features = features
+        self.tensors = {}
+        for name, arr in arrs.items():
+            raw = np.ascontiguousarray(arr).view(np.uint8).copy()
+            self.tensors[name] = torch.from_numpy(raw).to(device) if raw.size else None
+        self.task_count = int(arrs["tasks"].shape[0])
+        windows = int(arrs["window_offsets"].shape[0]) - 1
+        k = fmt.partial_count
+        if k:
+            self.partials = torch.empty(k * 8 * features, dtype=torch.float32, device=device)
+            self.counters = torch.zeros(windows * (features // 128), dtype=torch.int32,
+                                        device=device)
+        else:
+            self.partials = self.counters = None
+        t = self.tensors
+        self.view = DeviceView(
+            _ptr(t["window_offsets"]), _ptr(t["source_ids"]), _ptr(t["row_group_masks"]),
+            _ptr(t["source_metadata"]), _ptr(t["values"]), _ptr(t["bucket_offsets"]),
+            _ptr(t["tasks"]), _ptr(t["reductions"]), _ptr(t["partial_ids"]), self.task_count)
+
+    def workspace(self) -> SpmmWorkspace:
+        return SpmmWorkspace(self.partials, self.counters)
+
+    def spmm(self, packed_x: torch.Tensor, scales: torch.Tensor, output: torch.Tensor | None = None,
+             stream=None) -> torch.Tensor:
+        if output is None:
+            output = torch.empty((self.rows, self.features), dtype=torch.float32,
+                                 device=packed_x.device)
+        launch_spmm_int8(self.view, packed_x, scales, output, self.rows, self.cols, self.features,
+                         self.workspace(), stream)
+        return output
+
+
+class NativeDeviceMatrix:
+    """DeviceMatrix owned by the library (tcc_device_matrix_*): hipMalloc'd arrays + workspace."""
+
+    def __init__(self, fmt: Sw32HostFormat, features: int):
+        self._h = C.c_void_p()
+        check(lib().tcc_device_matrix_create(fmt.handle, features, C.byref(self._h)))
+        self.view = DeviceView()
+        p, c = C.c_void_p(), C.c_void_p()
+        check(lib().tcc_device_matrix_view(self._h, C.byref(self.view), C.byref(p), C.byref(c)))
+        self.partials_ptr, self.counters_ptr = p.value or 0, c.value or 0
+        self.rows, self.cols, self.features = fmt.rows, fmt.cols, features
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().tcc_device_matrix_free(self._h)
+            self._h = None
+
+    def spmm(self, packed_x: torch.Tensor, scales: torch.Tensor, output: torch.Tensor,
+             stream=None) -> torch.Tensor:
+        check(lib().tcc_launch_spmm_int8(C.byref(self.view), _ptr(packed_x), _ptr(scales),
+                                         _ptr(output), self.rows, self.cols, self.features,
+                                         self.partials_ptr, self.counters_ptr,
+                                         _stream_ptr(stream)))
+        return output

@@ -1,0 +1,44 @@
+"""Shared helpers for the GPU parity tests: run the HIP path through the C ABI and the C oracle on
+the same seeded inputs, and compare."""
+from __future__ import annotations
+
+import numpy as np
+
+import tcc_spmm_amd as T
+
+ATOL, RTOL = 1e-3, 1e-4  # |y - y_ref| <= ATOL + RTOL * |y_ref|  (north-star tolerance)
+
+
+def features(sources, feats, seed, stddev=1.0, outlier_fraction=0.0, outlier_scale=1.0):
+    return T.synth_features(sources, feats, seed, stddev, outlier_fraction, outlier_scale)
+
+
+def gpu_prepare(x_host: np.ndarray, device):
+    """Quantize and pack X on the GPU through the C ABI; returns device tensors + host copies."""
+    import torch
+    from tcc_spmm_amd.device import pack_features_int8x16, quantize_features_int8
+    x = torch.from_numpy(np.ascontiguousarray(x_host)).to(device)
+    q, scale = quantize_features_int8(x)
+    packed = pack_features_int8x16(q)
+    torch.cuda.synchronize()
+    return packed, scale, q.cpu().numpy(), scale.cpu().numpy(), packed.cpu().numpy()
+
+
+def assert_close(y, y_ref, what=""):
+    y = np.asarray(y, np.float64)
+    err = np.abs(y - y_ref)
+    bound = ATOL + RTOL * np.abs(y_ref)
+    bad = ~(err <= bound)
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} elements out of tolerance, max err "
+                             f"{float(np.nanmax(err))}, first {idx.tolist()} "
+                             f"got {[float(y[tuple(i)]) for i in idx]} "
+                             f"want {[float(y_ref[tuple(i)]) for i in idx]}")
+
+
+def check_features(oracle, x_host, q, scale, packed):
+    q_ref, s_ref = oracle.quantize(x_host)
+    assert np.array_equal(scale.view(np.uint32), s_ref.view(np.uint32)), "scales differ"
+    assert np.array_equal(q, q_ref), "quantized features differ"
+    assert np.array_equal(packed, oracle.pack16(q_ref)), "packed16 bytes differ"

@@ -1,0 +1,62 @@
+"""The C-ABI library loads on a CPU-only host and exports every symbol include/*.h declares."""
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def declared_functions():
+    text = (ROOT / "include" / "tcc_spmm_c.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tcc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for required in ("tcc_launch_spmm_int8", "tcc_quantize_features_int8",
+                     "tcc_pack_features_int8x16", "tcc_convert_csr_to_sw32",
+                     "tcc_build_panel_tasks", "tcc_make_canonical_csr"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from tcc_spmm_amd._lib import LIB_PATH, SIGNATURES
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in tcc_spmm_c.h but not exported"
+    assert set(declared_functions()) == set(SIGNATURES), "ctypes table out of sync with header"
+
+
+def test_version_and_error_reporting():
+    from tcc_spmm_amd._lib import check, lib
+    assert b"gfx950" in lib().tcc_version()
+    h = ctypes.c_void_p()
+    st = lib().tcc_synth_csr(b"no-such-config", ctypes.byref(ctypes.c_uint32()),
+                             ctypes.byref(ctypes.c_uint32()), ctypes.byref(h))
+    assert st == 1
+    assert b"unknown synthetic config" in lib().tcc_last_error()
+    with pytest.raises(ValueError):
+        check(st)
+
+
+def test_device_entry_points_reject_bad_features_before_any_launch():
+    # std::invalid_argument for F not in {128, 256} is raised before touching the GPU, so this
+    # runs on a CPU-only host (reference src/kernel/spmm.cu:20-29).
+    from tcc_spmm_amd._lib import DeviceView, lib
+    view = DeviceView()
+    view.taskCount = 1
+    st = lib().tcc_launch_spmm_int8(ctypes.byref(view), None, None, None, 32, 32, 64, None, None,
+                                    None)
+    assert st == 1
+    assert b"128 or 256" in lib().tcc_last_error()
+    st = lib().tcc_pack_features_int8x16(None, None, 4, 24, None)
+    assert st == 1  # features % 16 != 0
+
+
+def test_header_structs_match_cpp_layouts():
+    from tcc_spmm_amd._lib import DeviceView
+    assert ctypes.sizeof(DeviceView) == 10 * 8  # 9 pointers + uint32 padded to 8
+    header = (ROOT / "include" / "format" / "sw32.h").read_text()
+    assert "static_assert(sizeof(Sw32Task) == 28" in header

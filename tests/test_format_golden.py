@@ -1,0 +1,147 @@
+"""Host format parity: product builder and C oracle against the reference's own bytes.
+
+Fixtures (tests/golden/format_reference.npz) hold inputs and the outputs of the reference's
+makeCanonicalCsr / convertCsrToSw32 / loadMatrixMarket compiled from its sources
+(tests/golden/make_fixtures.py). Bit-exact comparison of every array.
+"""
+import numpy as np
+import pytest
+
+import tcc_spmm_amd as T
+
+FIELDS = ("window_offsets", "source_ids", "row_group_masks", "source_metadata", "values",
+          "bucket_offsets", "tasks", "reductions", "partial_ids")
+
+
+def _cases(golden, key):
+    return [str(x) for x in golden[f"index/{key}"]]
+
+
+def _same_bytes(a, b):
+    a = np.ascontiguousarray(a).view(np.uint8)
+    b = np.ascontiguousarray(b).view(np.uint8)
+    return a.shape == b.shape and bool((a == b).all())
+
+
+def test_fixture_inventory(golden):
+    assert len(_cases(golden, "format_cases")) >= 20
+    assert len(_cases(golden, "error_cases")) >= 6
+    assert len(_cases(golden, "mtx_cases")) >= 6
+
+
+@pytest.mark.parametrize("bucket", [1, 0])
+def test_product_builder_matches_reference_bytes(golden, bucket):
+    for name in _cases(golden, "format_cases"):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        csr = T.make_canonical_csr(rows, cols, golden[f"{name}/in_offsets"],
+                                   golden[f"{name}/in_sources"], golden[f"{name}/in_values"])
+        assert _same_bytes(csr.row_offsets, golden[f"{name}/csr_offsets"]), name
+        assert _same_bytes(csr.source_ids, golden[f"{name}/csr_sources"]), name
+        assert _same_bytes(csr.values, golden[f"{name}/csr_values"]), name
+        fmt = T.convert_csr_to_sw32(rows, cols, csr, bool(bucket))
+        arrs = fmt.arrays()
+        for f in FIELDS:
+            assert _same_bytes(arrs[f], golden[f"{name}/b{bucket}/{f}"]), (name, f)
+        assert fmt.partial_count == int(golden[f"{name}/b{bucket}/partial_count"][0]), name
+
+
+@pytest.mark.parametrize("bucket", [1, 0])
+def test_oracle_matches_reference_bytes(golden, oracle, bucket):
+    for name in _cases(golden, "format_cases"):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        off, src, val = oracle.canonical_csr(rows, cols, golden[f"{name}/in_offsets"],
+                                             golden[f"{name}/in_sources"],
+                                             golden[f"{name}/in_values"])
+        assert _same_bytes(off, golden[f"{name}/csr_offsets"]), name
+        assert _same_bytes(src, golden[f"{name}/csr_sources"]), name
+        assert _same_bytes(val, golden[f"{name}/csr_values"]), name
+        fmt = oracle.sw32(rows, cols, off, src, val, bool(bucket))
+        arrs = fmt.arrays()
+        for f in FIELDS:
+            assert _same_bytes(arrs[f], golden[f"{name}/b{bucket}/{f}"]), (name, f)
+        assert fmt.partial_count == int(golden[f"{name}/b{bucket}/partial_count"][0]), name
+
+
+def test_build_panel_tasks_replans_identically(golden):
+    for name in _cases(golden, "format_cases"):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        csr = T.make_canonical_csr(rows, cols, golden[f"{name}/csr_offsets"],
+                                   golden[f"{name}/csr_sources"], golden[f"{name}/csr_values"])
+        fmt = T.convert_csr_to_sw32(rows, cols, csr)
+        fmt.build_panel_tasks()
+        fmt.build_panel_tasks()
+        arrs = fmt.arrays()
+        for f in ("tasks", "reductions", "partial_ids"):
+            assert _same_bytes(arrs[f], golden[f"{name}/b1/{f}"]), (name, f)
+
+
+def test_build_panel_tasks_needs_bucketed_format(golden):
+    name = _cases(golden, "format_cases")[-1]
+    rows, cols = (int(x) for x in golden[f"{name}/dims"])
+    csr = T.make_canonical_csr(rows, cols, golden[f"{name}/csr_offsets"],
+                               golden[f"{name}/csr_sources"], golden[f"{name}/csr_values"])
+    fmt = T.convert_csr_to_sw32(rows, cols, csr, bucket_by_rw_mask=False)
+    with pytest.raises(ValueError):
+        fmt.build_panel_tasks()
+
+
+STATUS_TO_EXC = {1: ValueError, 2: OverflowError, 3: RuntimeError}
+
+
+def test_canonical_csr_errors_match_reference_classes(golden, oracle):
+    for name in _cases(golden, "error_cases"):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        status = int(golden[f"{name}/status"][0])
+        assert status != 0, name
+        args = (golden[f"{name}/in_offsets"], golden[f"{name}/in_sources"],
+                golden[f"{name}/in_values"])
+        with pytest.raises(STATUS_TO_EXC[status]):
+            T.make_canonical_csr(rows, cols, *args)
+        if rows and golden[f"{name}/in_offsets"].size == rows + 1:
+            from oracle import OracleError
+            with pytest.raises(OracleError) as e:
+                oracle.canonical_csr(rows, cols, *args)
+            assert e.value.code == status, name
+
+
+def test_conversion_errors_match_reference_classes(golden, oracle):
+    from oracle import OracleError
+    for name in _cases(golden, "conv_error_cases"):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        status = int(golden[f"{name}/status"][0])
+        assert status == 1, name
+        off, src, val = (golden[f"{name}/in_offsets"], golden[f"{name}/in_sources"],
+                         golden[f"{name}/in_values"])
+        raw = T.csr_from_arrays(rows, cols, off, src, val)
+        with pytest.raises(STATUS_TO_EXC[status]):
+            T.convert_csr_to_sw32(rows, cols, raw)
+        with pytest.raises(OracleError) as e:
+            oracle.sw32(rows, cols, off, src, val)
+        assert e.value.code == status, name
+
+
+def test_conversion_rejects_malformed_csr_struct():
+    # Offsets that disagree with the entry arrays (reference src/format/sw32.cpp:71-77).
+    with pytest.raises(ValueError):
+        T.convert_csr_to_sw32(2, 4, T.csr_from_arrays(2, 4, [0, 1], [0], [1.0]))
+    with pytest.raises(ValueError):
+        T.convert_csr_to_sw32(2, 4, T.csr_from_arrays(2, 4, [0, 2, 1], [0, 1], [1.0, 1.0]))
+    with pytest.raises(ValueError):
+        T.convert_csr_to_sw32(0, 4, T.csr_from_arrays(0, 4, [0], [], []))
+
+
+def test_matrix_market_matches_reference(golden, tmp_path):
+    for name in _cases(golden, "mtx_cases"):
+        p = tmp_path / f"{name}.mtx"
+        p.write_bytes(golden[f"{name}/text"].tobytes())
+        status = int(golden[f"{name}/status"][0])
+        if status:
+            with pytest.raises(STATUS_TO_EXC[status]):
+                T.load_matrix_market(p)
+            continue
+        csr = T.load_matrix_market(p)
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        assert (csr.rows, csr.cols) == (rows, cols)
+        assert _same_bytes(csr.row_offsets, golden[f"{name}/csr_offsets"]), name
+        assert _same_bytes(csr.source_ids, golden[f"{name}/csr_sources"]), name
+        assert _same_bytes(csr.values, golden[f"{name}/csr_values"]), name

@@ -1,0 +1,190 @@
+"""GPU parity: the HIP path (through the C ABI) against the C oracle on the same seeded inputs.
+
+Features: quantized scales and INT8 values and the packed16 bytes must be bit-identical.
+SpMM: |Y - Y_ref| <= 1e-3 + 1e-4 |Y_ref| against the oracle's TF32-operand sum accumulated in
+double. Protocol invariants: every Y element overwritten, counters back to zero, partials content
+irrelevant, repeated launches bitwise identical.
+"""
+import numpy as np
+import pytest
+
+import tcc_spmm_amd as T
+from gpu_cases import assert_close, check_features, features, gpu_prepare
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(fmt, packed, scale, feats, device, poison=True):
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    dm = TorchDeviceMatrix(fmt, feats, device=device)
+    y = torch.full((dm.rows, feats), float("nan"), device=device)
+    if dm.partials is not None and poison:
+        dm.partials.fill_(float("nan"))
+    dm.spmm(packed, scale, y)
+    torch.cuda.synchronize()
+    if dm.counters is not None:
+        assert int(dm.counters.abs().sum()) == 0, "completion counters must return to zero"
+    return dm, y.cpu().numpy()
+
+
+def _golden_names(golden):
+    return [str(x) for x in golden["index/format_cases"]]
+
+
+@pytest.mark.parametrize("shape", [(1, 16), (37, 48), (1000, 128), (513, 256), (64, 1024)])
+def test_quantize_and_pack_bit_exact(oracle, gpu, shape):
+    s, f = shape
+    x = features(s, f, seed=11 + s, stddev=3.0, outlier_fraction=0.05, outlier_scale=100.0)
+    x[0] = 0.0  # all-zero row -> scale 1, q = 0
+    if s > 2:
+        x[1, :] = np.float32(0.5) * np.arange(f, dtype=np.float32)  # many exact .5 quotients
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    check_features(oracle, x, q, sc, pk)
+    assert sc[0] == 1.0 and not q[0].any()
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_golden_format_cases(oracle, golden, gpu, feats):
+    for name in _golden_names(golden):
+        rows, cols = (int(x) for x in golden[f"{name}/dims"])
+        off, src, val = (golden[f"{name}/csr_offsets"], golden[f"{name}/csr_sources"],
+                         golden[f"{name}/csr_values"])
+        fmt = T.convert_csr_to_sw32(rows, cols, T.make_canonical_csr(rows, cols, off, src, val))
+        x = features(cols, feats, seed=rows * 7 + cols, stddev=2.0)
+        packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+        _, y = _run(fmt, packed, scale, feats, gpu)
+        y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
+        assert_close(y, y_ref, f"{name} F{feats}")
+
+
+def test_spmm_c1(oracle, gpu):
+    csr = T.synth_csr("c1")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, 128, seed=0)
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    check_features(oracle, x, q, sc, pk)
+    _, y = _run(fmt, packed, scale, 128, gpu)
+    off, src, val = csr.row_offsets, csr.source_ids, csr.values
+    y_ref = oracle.spmm_csr_f64(csr.rows, off, src, val, pk, sc, csr.cols)
+    assert_close(y, y_ref, "c1")
+
+
+def test_spmm_c2_full(oracle, gpu):
+    csr = T.synth_csr("c2")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    assert fmt.partial_count > 0
+    x = features(csr.cols, 128, seed=102)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    _, y = _run(fmt, packed, scale, 128, gpu)
+    y_ref = oracle.spmm_csr_f64(csr.rows, csr.row_offsets, csr.source_ids, csr.values, pk, sc,
+                                csr.cols)
+    assert_close(y, y_ref, "c2")
+
+
+def _sampled_windows(fmt, extra, count, seed):
+    tasks = fmt.tasks
+    split = np.unique(tasks["sw"][tasks["partial"] != T.NO_PARTIAL])
+    n_sw = len(fmt.window_offsets) - 1
+    rng = np.random.default_rng(seed)
+    pick = set(split[:: max(1, len(split) // (count // 2 or 1))].tolist())
+    pick |= set(rng.integers(0, n_sw, count).tolist()) | {0, n_sw - 1} | set(extra)
+    return np.array(sorted(pick), np.uint32)
+
+
+def _check_windows(oracle, csr, fmt, y, pk, sc, windows, what):
+    of = oracle.sw32(csr.rows, csr.cols, *csr.views())
+    y_ref = of.spmm_windows_f64(pk, sc, windows)
+    for i, w in enumerate(windows):
+        r0, r1 = int(w) * 32, min(csr.rows, int(w) * 32 + 32)
+        assert_close(y[r0:r1], y_ref[i * 32:i * 32 + (r1 - r0)], f"{what} SW {int(w)}")
+
+
+def test_spmm_c5_stress_f256(oracle, gpu):
+    csr = T.synth_csr("c5")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, 256, seed=105, stddev=2.0, outlier_fraction=0.01, outlier_scale=100.0)
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    check_features(oracle, x, q, sc, pk)
+    _, y = _run(fmt, packed, scale, 256, gpu)
+    assert np.isfinite(y).all(), "every output element must be overwritten"
+    windows = _sampled_windows(fmt, [], 300, seed=5)
+    _check_windows(oracle, csr, fmt, y, pk, sc, windows, "c5")
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_c3_sampled(oracle, gpu, feats):
+    csr = T.synth_csr("c3")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, feats, seed=103 if feats == 128 else 104)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    assert np.isfinite(y).all()
+    windows = _sampled_windows(fmt, [], 200, seed=3)
+    _check_windows(oracle, csr, fmt, y, pk, sc, windows, f"c3 F{feats}")
+
+
+def test_stream_reuse_and_overwrite(oracle, gpu):
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    # Split-heavy small case: two split SWs plus ordinary ones.
+    csr = T.synth_csr("t2000_40_9")
+    rng = np.random.default_rng(4)
+    off = csr.row_offsets.astype(np.int64)
+    src, val = csr.source_ids, csr.values
+    heavy = np.unique(rng.integers(0, csr.cols, 3500)).astype(np.uint32)
+    rows_cols = [src[off[r]:off[r + 1]] for r in range(csr.rows)]
+    rows_vals = [val[off[r]:off[r + 1]] for r in range(csr.rows)]
+    for r in (5, 40, 41):
+        rows_cols[r] = heavy
+        rows_vals[r] = rng.uniform(0.1, 1.0, heavy.size).astype(np.float32)
+    new_off = np.concatenate([[0], np.cumsum([len(c) for c in rows_cols])]).astype(np.uint32)
+    c2 = T.make_canonical_csr(csr.rows, csr.cols, new_off, np.concatenate(rows_cols),
+                              np.concatenate(rows_vals))
+    fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
+    assert fmt.partial_count > 0
+    x = features(c2.cols, 256, seed=77)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    dm = TorchDeviceMatrix(fmt, 256, device=gpu)
+    stream = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(stream):
+        for it in range(3):
+            y = torch.full((c2.rows, 256), float("nan"), device=gpu)
+            dm.partials.fill_(float("nan") if it % 2 == 0 else 1e30)
+            dm.spmm(packed, scale, y, stream=stream)
+            outs.append(y)
+    stream.synchronize()
+    assert int(dm.counters.abs().sum()) == 0
+    y0 = outs[0].cpu().numpy()
+    for y in outs[1:]:
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), y0.view(np.uint32))
+    y_ref = oracle.sw32(c2.rows, c2.cols, *c2.views()).spmm_f64(pk, sc)
+    assert_close(y0, y_ref, "stream reuse")
+
+
+def test_native_device_matrix_matches_torch_upload(gpu):
+    import torch
+    from tcc_spmm_amd.device import NativeDeviceMatrix
+    csr = T.synth_csr("c1")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, 128, seed=1)
+    packed, scale, _, _, _ = gpu_prepare(x, gpu)
+    _, y_torch = _run(fmt, packed, scale, 128, gpu)
+    nm = NativeDeviceMatrix(fmt, 128)
+    y = torch.empty((csr.rows, 128), device=gpu)
+    nm.spmm(packed, scale, y)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), y_torch.view(np.uint32))
+
+
+def test_bad_feature_count_raises_before_launch(gpu):
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix, launch_spmm_int8
+    csr = T.synth_csr("t64_4_1")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    dm = TorchDeviceMatrix(fmt, 128, device=gpu)
+    y = torch.zeros((64, 64), device=gpu)
+    with pytest.raises(ValueError):
+        launch_spmm_int8(dm.view, torch.zeros((64, 64), dtype=torch.int8, device=gpu),
+                         torch.ones(64, device=gpu), y, 64, 64, 64)
