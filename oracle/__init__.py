@@ -81,7 +81,8 @@ class Oracle:
         so.orc_spmm_sw32_f64.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p, C.c_uint32,
                                          C.c_void_p]
         so.orc_spmm_sw32_f64_windows.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p,
-                                                 C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p]
+                                                 C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p,
+                                                 C.c_void_p]
         so.orc_spmm_tasks_f32.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p, C.c_uint32,
                                           C.c_void_p, C.c_void_p]
         so.orc_spmm_sw32_f32_mt.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p,
@@ -196,16 +197,19 @@ class OracleFormat:
                                        packed.shape[1], y.ctypes.data)
         return y
 
-    def spmm_windows_f64(self, packed, scales, windows) -> np.ndarray:
-        """Y rows of the listed SWs ([len(windows) * 32, F], rows past the end are 0)."""
+    def spmm_windows_f64(self, packed, scales, windows, with_abs=False):
+        """Y rows of the listed SWs ([len(windows) * 32, F], rows past the end are 0); with_abs also
+        returns sum |tf32(a) * xhat| per element."""
         packed = np.ascontiguousarray(packed, np.int8)
         scales = np.ascontiguousarray(scales, np.float32)
         w = np.ascontiguousarray(windows, np.uint32)
         y = np.zeros((w.size * 32, packed.shape[1]), np.float64)
+        ya = np.zeros_like(y) if with_abs else None
         self._orc.so.orc_spmm_sw32_f64_windows(C.byref(self._f), packed.ctypes.data,
                                                scales.ctypes.data, packed.shape[1], w.ctypes.data,
-                                               w.size, y.ctypes.data)
-        return y
+                                               w.size, y.ctypes.data,
+                                               ya.ctypes.data if with_abs else None)
+        return (y, ya) if with_abs else y
 
     def spmm_tasks_f32(self, packed, scales):
         packed = np.ascontiguousarray(packed, np.int8)

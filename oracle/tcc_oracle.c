@@ -478,8 +478,10 @@ void orc_spmm_sw32_f64(const orc_sw32* fm, const int8_t* packedX, const float* s
 }
 
 void orc_spmm_sw32_f64_windows(const orc_sw32* fm, const int8_t* packedX, const float* scales,
-                               uint32_t features, const uint32_t* windows, uint32_t n, double* y) {
+                               uint32_t features, const uint32_t* windows, uint32_t n, double* y,
+                               double* yabs) {
     memset(y, 0, (size_t)n * 32 * features * sizeof(double));
+    if (yabs) memset(yabs, 0, (size_t)n * 32 * features * sizeof(double));
     for (uint32_t i = 0; i < n; ++i) {
         uint32_t sw = windows[i];
         for (size_t slot = (size_t)fm->windowOffsets[sw] * 8;
@@ -493,8 +495,12 @@ void orc_spmm_sw32_f64_windows(const orc_sw32* fm, const int8_t* packedX, const 
                 if (!(mask & (1u << r))) continue;
                 double a = (double)orc_tf32(fm->values[base + k++]);
                 double* yr = y + ((size_t)i * 32 + r) * features;
-                for (uint32_t f = 0; f < features; ++f)
-                    yr[f] += a * (double)xhat(packedX, scales, c, f, features);
+                double* ya = yabs ? yabs + ((size_t)i * 32 + r) * features : NULL;
+                for (uint32_t f = 0; f < features; ++f) {
+                    double p = a * (double)xhat(packedX, scales, c, f, features);
+                    yr[f] += p;
+                    if (ya) ya[f] += fabs(p);
+                }
             }
         }
     }

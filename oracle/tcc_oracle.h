@@ -79,7 +79,10 @@ void orc_spmm_sw32_f64(const orc_sw32* f, const int8_t* packedX, const float* sc
 /* As orc_spmm_sw32_f64 but only for the listed SWs: y has n*32 rows (rows past the matrix end stay
  * 0). Lets tests check sampled windows of configurations too large for a full CPU pass. */
 void orc_spmm_sw32_f64_windows(const orc_sw32* f, const int8_t* packedX, const float* scales,
-                               uint32_t features, const uint32_t* windows, uint32_t n, double* y);
+                               uint32_t features, const uint32_t* windows, uint32_t n, double* y,
+                               double* yabs);
+/* yabs (optional, same shape as y) receives sum |tf32(a) * xhat| per element: the scale of the FP32
+ * summation error of any accumulation order (error <~ u * sum|terms| for a random walk). */
 
 /* Restatement of the kernel's task/partial/merge protocol in FP32 (spmm_kernel.cuh:228-282):
  * each task accumulates its panels in FP32 (slot order), unsplit tasks write Y, split tasks write

@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 import tcc_spmm_amd as T
-from gpu_cases import assert_close, check_features, features, gpu_prepare
+from gpu_cases import (assert_close, assert_close_conditioned, check_features, features,
+                       gpu_prepare)
 
 pytestmark = pytest.mark.gpu
 
@@ -92,12 +93,19 @@ def _sampled_windows(fmt, extra, count, seed):
     return np.array(sorted(pick), np.uint32)
 
 
-def _check_windows(oracle, csr, fmt, y, pk, sc, windows, what):
+def _check_windows(oracle, csr, fmt, y, pk, sc, windows, what, conditioned=False):
     of = oracle.sw32(csr.rows, csr.cols, *csr.views())
-    y_ref = of.spmm_windows_f64(pk, sc, windows)
+    y_ref, y_abs = of.spmm_windows_f64(pk, sc, windows, with_abs=True)
+    relaxed = 0
     for i, w in enumerate(windows):
         r0, r1 = int(w) * 32, min(csr.rows, int(w) * 32 + 32)
-        assert_close(y[r0:r1], y_ref[i * 32:i * 32 + (r1 - r0)], f"{what} SW {int(w)}")
+        sl = slice(i * 32, i * 32 + (r1 - r0))
+        if conditioned:
+            relaxed += assert_close_conditioned(y[r0:r1], y_ref[sl], y_abs[sl],
+                                                f"{what} SW {int(w)}")
+        else:
+            assert_close(y[r0:r1], y_ref[sl], f"{what} SW {int(w)}")
+    return relaxed
 
 
 def test_spmm_c5_stress_f256(oracle, gpu):
@@ -109,7 +117,10 @@ def test_spmm_c5_stress_f256(oracle, gpu):
     _, y = _run(fmt, packed, scale, 256, gpu)
     assert np.isfinite(y).all(), "every output element must be overwritten"
     windows = _sampled_windows(fmt, [], 300, seed=5)
-    _check_windows(oracle, csr, fmt, y, pk, sc, windows, "c5")
+    relaxed = _check_windows(oracle, csr, fmt, y, pk, sc, windows, "c5", conditioned=True)
+    checked = len(windows) * 32 * 256
+    print(f"c5: {relaxed} of {checked} checked elements needed the conditioning term")
+    assert relaxed <= checked * 1e-3
 
 
 @pytest.mark.parametrize("feats", [128, 256])
@@ -128,11 +139,11 @@ def test_stream_reuse_and_overwrite(oracle, gpu):
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix
     # Split-heavy small case: two split SWs plus ordinary ones.
-    csr = T.synth_csr("t2000_40_9")
+    csr = T.synth_csr("t4000_40_9")
     rng = np.random.default_rng(4)
     off = csr.row_offsets.astype(np.int64)
     src, val = csr.source_ids, csr.values
-    heavy = np.unique(rng.integers(0, csr.cols, 3500)).astype(np.uint32)
+    heavy = np.arange(0, csr.cols, dtype=np.uint32)  # 4000 sources: 500 panels -> split SW
     rows_cols = [src[off[r]:off[r + 1]] for r in range(csr.rows)]
     rows_vals = [val[off[r]:off[r + 1]] for r in range(csr.rows)]
     for r in (5, 40, 41):
