@@ -41,6 +41,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr unsigned kWave = 64;
 constexpr unsigned kSlice = 128;
 constexpr unsigned kNoPartial = 0xFFFFFFFFu;
+// Row-group set of bucket slot s (sw32BucketOrder, include/format/sw32.h).
+__constant__ unsigned kBucketRwSet[16] = {0, 1, 2, 4, 8, 3, 5, 6, 7, 9, 10, 11, 12, 13, 14, 15};
 
 // TF32 rounding from its definition: keep 10 explicit mantissa bits, round to nearest with ties
 // away from zero (adding half an ulp to the sign-magnitude encoding), carry into the exponent.
@@ -58,54 +60,189 @@ struct KernelArgs {
     float* partials;
     unsigned* counters;
     unsigned rows, cols;
+    unsigned xBytes; // cols * features (< 2^32, checked by the launcher)
 };
 
-// Dense A-value table for one row group of one panel: lane (k = l/8, r = l%8).
-__device__ __forceinline__ void expandPanelRows(const KernelArgs& a, unsigned panel, unsigned rw,
-                                                unsigned lane, float* table) {
-    const unsigned k = lane >> 3, r = lane & 7;
-    const std::uint64_t meta = a.m.sourceMetadata[std::size_t(panel) * 8 + k];
-    const unsigned mask = unsigned(meta), base = unsigned(meta >> 32);
-    const unsigned row = rw * 8 + r;
-    const bool present = (mask >> row) & 1u;
-    // Padding slots have mask 0 and base 0; every other slot owns >= 1 value at `base`.
-    const unsigned idx = present ? base + __popc(mask & ((1u << row) - 1u)) : base;
-    const float v = a.m.values[idx];
-    table[lane] = present ? roundTf32(v) : 0.0f;
+// ---------------------------------------------------------------------------------------------
+// Panel pipeline. Inside one phase (the exclusive buckets 1..4, or the shared buckets 5..15) the
+// panels of a task are walked in order with a three-stage software pipeline whose per-iteration
+// memory operations are identical on every path, so the compiler's wait counters stay exact:
+//   stage 1 (panel p+2): lane (k = l/8, r = l%8) loads slot k's source id and metadata;
+//   stage 2 (panel p+1): its scale, its A value(s) for row r of the panel's row groups, and the X
+//                        gathers of the 8 slots (one 128-byte slice per slot, SGPR row offset);
+//   stage 3 (panel p):   A values -> TF32 -> LDS table, dequantize X, MFMA accumulate.
+// Panel indices past the phase end are clamped to its last panel (harmless duplicate loads).
+
+struct Meta {
+    unsigned id;
+    unsigned mask;
+    unsigned base;
+};
+
+struct Stage2 {
+    unsigned src;    // clamped source id of slot k (row 0 for padding)
+    float scale;     // scale of that source
+    float v[4];      // raw A values of (slot k, row 8g + r), g = the panel's row groups
+    unsigned bits;   // bit g set when slot k touches row 8g + r
+    unsigned xr[8];  // X byte pairs of the 8 slots for this lane's features
+};
+
+__device__ __forceinline__ Meta loadMeta(const KernelArgs& a, unsigned panel, unsigned lane) {
+    const std::size_t slot = std::size_t(panel) * 8 + (lane >> 3);
+    const std::uint64_t md = a.m.sourceMetadata[slot];
+    return {a.m.sourceIds[slot], unsigned(md), unsigned(md >> 32)};
 }
 
-template <unsigned RWSET>
-__device__ __forceinline__ void accumulatePanels(const KernelArgs& a, unsigned begin, unsigned end,
-                                                 unsigned lane, unsigned xOffset, unsigned features,
-                                                 float (*table)[64], f32x4 (&acc)[2][8]) {
-    for (unsigned panel = begin; panel < end; ++panel) {
+// Value of (slot, row) or the slot's first value when the row is absent (always a valid index:
+// padding slots have base 0 and the matrix has at least one value when it has panels).
+__device__ __forceinline__ float loadValue(const KernelArgs& a, const Meta& m, unsigned row,
+                                           bool& present) {
+    present = (m.mask >> row) & 1u;
+    const unsigned idx = m.base + __popc(m.mask & ((1u << row) - 1u));
+    return a.m.values[present ? idx : m.base];
+}
+
+template <unsigned NG>
+__device__ __forceinline__ void loadStage2(const KernelArgs& a, const Meta& m, const unsigned* rws,
+                                           unsigned lane, __amdgpu_buffer_rsrc_t xr,
+                                           unsigned xLane, unsigned features, Stage2& s) {
+    const bool live = m.id < a.cols;
+    s.src = live ? m.id : 0u;
+    s.scale = a.scales[s.src];
+    s.bits = 0;
 #pragma unroll
-        for (unsigned rw = 0; rw < 4; ++rw)
-            if (RWSET & (1u << rw)) expandPanelRows(a, panel, rw, lane, table[rw]);
-        __syncthreads();
-        const unsigned* ids = a.m.sourceIds + std::size_t(panel) * 8;
+    for (unsigned g = 0; g < NG; ++g) {
+        bool present;
+        s.v[g] = loadValue(a, m, rws[g] * 8 + (lane & 7), present);
+        s.bits |= unsigned(present && live) << g;
+    }
 #pragma unroll
-        for (unsigned k = 0; k < 8; ++k) {
-            const unsigned src = ids[k];
-            if (src >= a.cols) continue; // padding slot (always at the end of a bucket)
-            const unsigned short pair = *reinterpret_cast<const unsigned short*>(
-                a.packedX + std::size_t(src) * features + xOffset);
-            const float s = a.scales[src];
-            const float x0 = roundTf32(float(std::int8_t(pair & 0xFFu)) * s);
-            const float x1 = roundTf32(float(std::int8_t(pair >> 8)) * s);
+    for (unsigned j = 0; j < 8; ++j) {
+        const unsigned src = __builtin_amdgcn_readlane(s.src, j * 8);
+        s.xr[j] = __builtin_amdgcn_raw_buffer_load_b16(xr, xLane, src * features, 0);
+    }
+}
+
+// Accumulate one panel whose row groups are rws[0..NG) (NG = 4 in the shared phase, where only the
+// groups in `rwset` are computed).
+template <unsigned NG>
+__device__ __forceinline__ void computeStage3(const Stage2& s, const unsigned* rws, unsigned rwset,
+                                              unsigned lane, float* table, f32x4 (&acc)[2][8]) {
+    // A table: table[g][k][r] = tf32(A[8*rws[g] + r][slot k]) (0 when absent).
 #pragma unroll
-            for (unsigned rw = 0; rw < 4; ++rw) {
-                if (!(RWSET & (1u << rw))) continue;
+    for (unsigned g = 0; g < NG; ++g)
+        table[g * 64 + lane] = ((s.bits >> g) & 1u) ? roundTf32(s.v[g]) : 0.0f;
+    __syncthreads();
+    float x0[8], x1[8];
 #pragma unroll
-                for (unsigned half = 0; half < 2; ++half) {
-                    const float av = table[rw][k * 8 + half * 4 + (lane & 3)];
-                    const unsigned quad = rw * 2 + half;
-                    acc[0][quad] = __builtin_amdgcn_mfma_f32_4x4x1f32(av, x0, acc[0][quad], 0, 0, 0);
-                    acc[1][quad] = __builtin_amdgcn_mfma_f32_4x4x1f32(av, x1, acc[1][quad], 0, 0, 0);
-                }
+    for (unsigned j = 0; j < 8; ++j) {
+        const float sc =
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s.scale), j * 8));
+        x0[j] = roundTf32(float(std::int8_t(s.xr[j] & 0xFFu)) * sc);
+        x1[j] = roundTf32(float(std::int8_t(s.xr[j] >> 8)) * sc);
+    }
+#pragma unroll
+    for (unsigned g = 0; g < NG; ++g) {
+        if (NG > 1 && !(rwset & (1u << g))) continue;
+        const unsigned rw = rws[g];
+        float a0[8], a1[8];
+#pragma unroll
+        for (unsigned j = 0; j < 8; ++j) {
+            a0[j] = table[g * 64 + j * 8 + (lane & 3)];
+            a1[j] = table[g * 64 + j * 8 + 4 + (lane & 3)];
+        }
+        // rw is uniform; the accumulator quads are selected by a uniform switch.
+#define TCC_MFMA_RW(R)                                                                           \
+    for (unsigned j = 0; j < 8; ++j) {                                                           \
+        acc[0][2 * R] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0[j], x0[j], acc[0][2 * R], 0, 0, 0);   \
+        acc[1][2 * R] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0[j], x1[j], acc[1][2 * R], 0, 0, 0);   \
+        acc[0][2 * R + 1] =                                                                      \
+            __builtin_amdgcn_mfma_f32_4x4x1f32(a1[j], x0[j], acc[0][2 * R + 1], 0, 0, 0);       \
+        acc[1][2 * R + 1] =                                                                      \
+            __builtin_amdgcn_mfma_f32_4x4x1f32(a1[j], x1[j], acc[1][2 * R + 1], 0, 0, 0);       \
+    }
+        if (NG > 1) {
+            if (g == 0) { TCC_MFMA_RW(0) }
+            else if (g == 1) { TCC_MFMA_RW(1) }
+            else if (g == 2) { TCC_MFMA_RW(2) }
+            else { TCC_MFMA_RW(3) }
+        } else {
+            switch (rw) {
+            case 0: TCC_MFMA_RW(0) break;
+            case 1: TCC_MFMA_RW(1) break;
+            case 2: TCC_MFMA_RW(2) break;
+            default: TCC_MFMA_RW(3) break;
             }
         }
-        __syncthreads();
+#undef TCC_MFMA_RW
+    }
+    __syncthreads();
+}
+
+// Row group of a panel in the exclusive phase: bucket slots 1..4 are RW0..RW3.
+__device__ __forceinline__ unsigned exclusiveGroup(const unsigned* slots, unsigned panel) {
+    return (panel >= slots[2]) + (panel >= slots[3]) + (panel >= slots[4]);
+}
+
+// Row-group set of a panel in the shared phase (bucket slots 5..15).
+__device__ __forceinline__ unsigned sharedGroups(const unsigned* slots, unsigned panel) {
+    unsigned s = 5;
+#pragma unroll
+    for (unsigned t = 6; t < 16; ++t) s += panel >= slots[t];
+    return kBucketRwSet[s];
+}
+
+__device__ __forceinline__ void exclusivePhase(const KernelArgs& a, const unsigned* slots,
+                                               unsigned begin, unsigned end, unsigned lane,
+                                               __amdgpu_buffer_rsrc_t xr, unsigned xLane,
+                                               unsigned features, float* table,
+                                               f32x4 (&acc)[2][8]) {
+    if (begin >= end) return;
+    const unsigned last = end - 1;
+    Meta m2 = loadMeta(a, begin, lane);
+    Meta m1 = loadMeta(a, min(begin + 1, last), lane);
+    unsigned g0 = exclusiveGroup(slots, begin);
+    Stage2 cur;
+    loadStage2<1>(a, m2, &g0, lane, xr, xLane, features, cur);
+    m2 = loadMeta(a, min(begin + 2, last), lane);
+#pragma unroll 1
+    for (unsigned p = begin; p < end; ++p) {
+        const unsigned q = min(p + 1, last);
+        unsigned gq = exclusiveGroup(slots, q);
+        Stage2 next;
+        loadStage2<1>(a, m1, &gq, lane, xr, xLane, features, next);
+        m1 = m2;
+        m2 = loadMeta(a, min(p + 3, last), lane);
+        computeStage3<1>(cur, &g0, 1u << g0, lane, table, acc);
+        cur = next;
+        g0 = gq;
+    }
+}
+
+__device__ __forceinline__ void sharedPhase(const KernelArgs& a, const unsigned* slots,
+                                            unsigned begin, unsigned end, unsigned lane,
+                                            __amdgpu_buffer_rsrc_t xr, unsigned xLane,
+                                            unsigned features, float* table,
+                                            f32x4 (&acc)[2][8]) {
+    if (begin >= end) return;
+    const unsigned last = end - 1;
+    const unsigned all[4] = {0, 1, 2, 3};
+    Meta m2 = loadMeta(a, begin, lane);
+    Meta m1 = loadMeta(a, min(begin + 1, last), lane);
+    Stage2 cur;
+    loadStage2<4>(a, m2, all, lane, xr, xLane, features, cur);
+    unsigned set0 = sharedGroups(slots, begin);
+    m2 = loadMeta(a, min(begin + 2, last), lane);
+#pragma unroll 1
+    for (unsigned p = begin; p < end; ++p) {
+        const unsigned q = min(p + 1, last);
+        Stage2 next;
+        loadStage2<4>(a, m1, all, lane, xr, xLane, features, next);
+        m1 = m2;
+        m2 = loadMeta(a, min(p + 3, last), lane);
+        computeStage3<4>(cur, all, set0, lane, table, acc);
+        cur = next;
+        set0 = sharedGroups(slots, q);
     }
 }
 
@@ -119,7 +256,7 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
 
 template <unsigned Features>
 __global__ __launch_bounds__(kWave) void spmmInt8Kernel(KernelArgs a) {
-    __shared__ float table[4][64];
+    __shared__ __align__(16) float table[4 * 64];
     __shared__ unsigned lastFlag;
     const unsigned lane = threadIdx.x;
     const unsigned slice = blockIdx.y;
@@ -127,7 +264,7 @@ __global__ __launch_bounds__(kWave) void spmmInt8Kernel(KernelArgs a) {
     const Sw32Task task = a.m.tasks[taskIndex];
     const unsigned sw = task.sw;
     const unsigned f0 = 16 * (lane >> 3) + (lane & 7); // f1 = f0 + 8
-    const unsigned xOffset = slice * kSlice + 2 * lane;
+    const unsigned xLane = slice * kSlice + 2 * lane;
 
     f32x4 acc[2][8];
 #pragma unroll
@@ -136,28 +273,12 @@ __global__ __launch_bounds__(kWave) void spmmInt8Kernel(KernelArgs a) {
         for (unsigned q = 0; q < 8; ++q) acc[h][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const unsigned* slots = a.m.bucketOffsets + std::size_t(sw) * 17;
-#pragma unroll 1
-    for (unsigned s = 1; s < 16; ++s) {
-        const unsigned begin = max(slots[s], task.begin), end = min(slots[s + 1], task.end);
-        if (begin >= end) continue;
-        switch (s) {
-        case 1: accumulatePanels<1>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 2: accumulatePanels<2>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 3: accumulatePanels<4>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 4: accumulatePanels<8>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 5: accumulatePanels<3>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 6: accumulatePanels<5>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 7: accumulatePanels<6>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 8: accumulatePanels<7>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 9: accumulatePanels<9>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 10: accumulatePanels<10>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 11: accumulatePanels<11>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 12: accumulatePanels<12>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 13: accumulatePanels<13>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        case 14: accumulatePanels<14>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        default: accumulatePanels<15>(a, begin, end, lane, xOffset, Features, table, acc); break;
-        }
-    }
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<std::int8_t*>(a.packedX), 0, a.xBytes, 0x00020000);
+    exclusivePhase(a, slots, max(slots[1], task.begin), min(slots[5], task.end), lane, xr, xLane,
+                   Features, table, acc);
+    sharedPhase(a, slots, max(slots[5], task.begin), min(slots[16], task.end), lane, xr, xLane,
+                Features, table, acc);
 
     // Write-back: D of quad q holds rows 4q..4q+3 (vector element i = row 4q+i) for the lane's
     // feature column.
@@ -244,8 +365,10 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
         throw std::invalid_argument("feature dimension must be 128 or 256");
     if (!matrix.taskCount)
         throw std::runtime_error("launchSpmmInt8: invalid configuration argument (no tasks)");
-    const KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
-                          rows, cols};
+    if (std::uint64_t(cols) * features > 0xFFFFFFFFull)
+        throw std::invalid_argument("launchSpmmInt8: X must be smaller than 4 GiB (cols * features)");
+    const KernelArgs args{matrix,   packedX, scales, output, workspace.partials, workspace.counters,
+                          rows,     cols,    cols * features};
     if (features == 128)
         launch<128>(args, stream);
     else
