@@ -8,16 +8,13 @@
 //   32 FP32 registers per lane; at its end the rows are final (or a partial tile for split tasks).
 //
 // Lane layout
-//   X gathers: dword loads, two slots per instruction. Lane L (half H = L / 32, w = L % 32) loads
-//   bytes 4w..4w+3 of the slice row of slot i + 4H in load i (i = 0..3), i.e. features
-//   16t + {2m, 2m + 8, 2m + 1, 2m + 9} of the packed16 layout (t = w / 4, m = w % 4).
-//   Per-slot data: lane L holds slot k = (L & 3) | (H << 2) and row r = (L >> 2) & 7, so the DPP
-//   row broadcast `row_newbcast:i` hands every lane of 16-lane row R the value of slot i + 4*(R/2),
-//   which is exactly the slot its half loads in load i.
-//   MFMA v_mfma_f32_4x4x1_16b_f32: block b = lanes 4b..4b+3 (all in one half) computes
-//   4 rows x 4 lane features; A = the quad's 4 row values of the half's slot (LDS table),
-//   B = the lane's dequantized byte e, D = acc[quad][e]. The two halves hold partial sums of the
-//   same features (even/odd slot positions) and are added at the end of the pass.
+//   Per-slot data (metadata, scale, A table entries): lane L holds slot k = L & 7 and row
+//   r = (L >> 3) & 7, so the DPP row broadcast `row_newbcast:j` hands every lane slot j's value.
+//   X gathers: one dwordx4 load per panel, lane L fetching the 16-byte tile L & 7 of the 128-byte
+//   slice row of slot L >> 3 (eight rows per instruction). The tile is written to LDS and read back
+//   transposed: lane l then holds byte pair l (features 16(l/8) + l%8 and + 8) of all 8 slots.
+//   MFMA v_mfma_f32_4x4x1_16b_f32: A = the 4 row values of one quad of slot j (LDS table),
+//   B = the lane's dequantized feature, D = 4 rows x the lane's feature: acc[quad][feature].
 //
 // Per panel: the A values of (slot k, row 8g + r) are TF32-rounded into an LDS table [8][8]
 // (zero where the slot does not touch the row); X bytes are sign-extended to FP32 (SDWA),
@@ -43,17 +40,13 @@
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr unsigned kWave = 64;
 constexpr unsigned kSlice = 128;
 constexpr unsigned kNoPartial = 0xFFFFFFFFu;
 constexpr unsigned kEnd = 0xFFFFFFFFu;
-
-// Indexed buffer load: address = base + vindex * stride + voffset, range-checked on vindex.
-__device__ int bufferLoadIndexed(i32x4 rsrc, int vindex, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.struct.buffer.load.i32");
 
 // TF32 rounding from its definition: keep 10 explicit mantissa bits, round to nearest with ties
 // away from zero (adding half an ulp to the sign-magnitude encoding), carry into the exponent.
@@ -113,100 +106,93 @@ __device__ __forceinline__ unsigned panelCount(const Bounds& b) {
 // ------------------------------------------------------------------------------------------------
 // Pipeline stages
 
-struct Meta { // slot k(L) of one panel
-    unsigned id;
-    unsigned mask;
-    unsigned base;
+struct Meta {        // one panel
+    unsigned id;     // lane L: source of slot L & 7
+    unsigned mask;   // lane L: row mask of slot L & 7
+    unsigned base;   // lane L: value base of slot L & 7
+    unsigned gather; // lane L: source of slot L >> 3 (the row this lane gathers)
 };
 
-struct Stage2 {     // one panel, ready to compute
-    unsigned src;   // lane: clamped source id of slot k(L) (row 0 for padding)
-    float scale;    // lane: scale of that source
-    float v;        // lane: raw A value of (slot k(L), row 8G + r(L))
-    unsigned bits;  // 1 when slot k(L) touches that row
-    unsigned xr[4]; // X dwords of loads 0..3 for this lane
+struct Stage2 {   // one panel, ready to compute
+    float scale;  // lane L: scale of slot L & 7
+    float v;      // lane L: raw A value of (slot L & 7, row 8G + r)
+    unsigned bits;// 1 when slot L & 7 touches that row
+    u32x4 x;      // 16-byte tile L & 7 of the X row of slot L >> 3
 };
-
-__device__ __forceinline__ unsigned slotOf(unsigned lane) { return (lane & 3) | ((lane >> 5) << 2); }
 
 __device__ __forceinline__ Meta loadMeta(const KernelArgs& a, unsigned panel, unsigned lane) {
-    const std::size_t slot = std::size_t(panel) * 8 + slotOf(lane);
-    const std::uint64_t md = __builtin_nontemporal_load(a.m.sourceMetadata + slot);
-    return {__builtin_nontemporal_load(a.m.sourceIds + slot), unsigned(md), unsigned(md >> 32)};
+    const std::size_t first = std::size_t(panel) * 8;
+    const std::uint64_t md = __builtin_nontemporal_load(a.m.sourceMetadata + first + (lane & 7));
+    return {__builtin_nontemporal_load(a.m.sourceIds + first + (lane & 7)), unsigned(md),
+            unsigned(md >> 32), __builtin_nontemporal_load(a.m.sourceIds + first + (lane >> 3))};
 }
 
 template <unsigned G>
 __device__ __forceinline__ void loadStage2(const KernelArgs& a, const Meta& m, unsigned lane,
-                                           i32x4 xr, unsigned xLane, Stage2& s) {
+                                           const std::int8_t* xSlice, unsigned features,
+                                           Stage2& s) {
     const bool live = m.id < a.cols;
-    s.src = live ? m.id : 0u;
-    s.scale = a.scales[s.src];
-    const unsigned row = G * 8 + ((lane >> 2) & 7);
+    s.scale = a.scales[live ? m.id : 0u];
+    const unsigned row = G * 8 + ((lane >> 3) & 7);
     const bool present = live && ((m.mask >> row) & 1u);
     // The k-th set row bit of a slot owns values[base + k]; absent rows read values[base] (a valid
     // index: padding has base 0 and a matrix with panels has values).
     const unsigned idx = present ? m.base + __popc(m.mask & ((1u << row) - 1u)) : m.base;
     s.v = __builtin_nontemporal_load(a.m.values + idx);
     s.bits = present;
-    // Source row of the slot this lane's half loads in load i (slot i + 4H): DPP row broadcast.
-    s.xr[0] = unsigned(bufferLoadIndexed(
-        xr, __builtin_amdgcn_mov_dpp(int(s.src), 0x150, 0xF, 0xF, true), int(xLane), 0, 0));
-    s.xr[1] = unsigned(bufferLoadIndexed(
-        xr, __builtin_amdgcn_mov_dpp(int(s.src), 0x151, 0xF, 0xF, true), int(xLane), 0, 0));
-    s.xr[2] = unsigned(bufferLoadIndexed(
-        xr, __builtin_amdgcn_mov_dpp(int(s.src), 0x152, 0xF, 0xF, true), int(xLane), 0, 0));
-    s.xr[3] = unsigned(bufferLoadIndexed(
-        xr, __builtin_amdgcn_mov_dpp(int(s.src), 0x153, 0xF, 0xF, true), int(xLane), 0, 0));
+    const unsigned src = m.gather < a.cols ? m.gather : 0u;
+    s.x = *reinterpret_cast<const u32x4*>(xSlice + std::size_t(src) * features + 16 * (lane & 7));
 }
 
-// Dequantize load i: bytes 0..3 -> FP32 (sign-extended SDWA converts), times the scale of the
-// half's slot (DPP row broadcast of lane i of each 16-lane row), rounded to TF32. The s_nop covers
-// the VALU-write -> DPP-read hazard on the scale register.
-template <unsigned I>
-__device__ __forceinline__ void dequantize(unsigned w, float scale, float (&x)[4]) {
-    float q0, q1, q2, q3;
+// x_lo / x_hi of slot j = tf32(float(byte) * scale of slot j), for both bytes of the pair; the
+// scale comes from lane j of the lane's 16-lane row (DPP row broadcast). The s_nop covers the
+// VALU-write -> DPP-read hazard on the scale register.
+template <unsigned J>
+__device__ __forceinline__ void dequantPair(unsigned pair, float scale, float& lo, float& hi) {
+    float q0, q1;
     asm volatile(
-        "v_cvt_f32_i32_sdwa %0, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f32_i32_sdwa %2, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f32_i32_sdwa %3, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
         "s_nop 1\n\t"
-        "v_mul_f32_dpp %0, %5, %0 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %1, %5, %1 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %2, %5, %2 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %3, %5, %3 row_newbcast:%6 row_mask:0xf bank_mask:0xf"
-        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3)
-        : "v"(w), "v"(scale), "i"(I));
-    x[0] = roundTf32(q0);
-    x[1] = roundTf32(q1);
-    x[2] = roundTf32(q2);
-    x[3] = roundTf32(q3);
+        "v_mul_f32_dpp %0, %3, %0 row_newbcast:%4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %1, %3, %1 row_newbcast:%4 row_mask:0xf bank_mask:0xf"
+        : "=&v"(q0), "=&v"(q1)
+        : "v"(pair), "v"(scale), "i"(J));
+    lo = roundTf32(q0);
+    hi = roundTf32(q1);
 }
 
-template <unsigned I>
-__device__ __forceinline__ void accumulateLoad(const Stage2& s, const float* table,
-                                               unsigned tableLane, f32x4 (&acc)[2][4]) {
-    float x[4];
-    dequantize<I>(s.xr[I], s.scale, x);
-    // A of quad h for lane 4b+i: row 4h + i of the half's slot I + 4H.
-    const float a0 = table[tableLane + I];
-    const float a1 = table[tableLane + 32 + I];
-#pragma unroll
-    for (unsigned e = 0; e < 4; ++e) {
-        acc[0][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, x[e], acc[0][e], 0, 0, 0);
-        acc[1][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, x[e], acc[1][e], 0, 0, 0);
-    }
+template <unsigned J>
+__device__ __forceinline__ void accumulateSlot(const Stage2& s, const unsigned short* xt,
+                                               const float* table, unsigned quadRow,
+                                               f32x4 (&acc)[2][2]) {
+    float lo, hi;
+    dequantPair<J>(xt[J * 64], s.scale, lo, hi);
+    const float a0 = table[quadRow + J];      // rows 0..3 of the group (quad 0)
+    const float a1 = table[quadRow + 32 + J]; // rows 4..7 (quad 1)
+    acc[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, lo, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, hi, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, lo, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, hi, acc[1][1], 0, 0, 0);
 }
 
 __device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, float* table,
-                                              unsigned tableLane, f32x4 (&acc)[2][4]) {
-    // table[r][k] = tf32(A[row 8G + r][slot k]), 0 when absent.
-    table[((lane >> 2) & 7) * 8 + slotOf(lane)] = s.bits ? roundTf32(s.v) : 0.0f;
+                                              u32x4* xtile, f32x4 (&acc)[2][2]) {
+    // table[r][k] = tf32(A[row 8G + r][slot k]), 0 when absent; the X tiles go to LDS in row order
+    // and come back as byte pair `lane` of each slot row: xt[j * 64] = pair of slot j.
+    table[lane] = s.bits ? roundTf32(s.v) : 0.0f;
+    xtile[lane] = s.x;
     __syncthreads();
-    accumulateLoad<0>(s, table, tableLane, acc);
-    accumulateLoad<1>(s, table, tableLane, acc);
-    accumulateLoad<2>(s, table, tableLane, acc);
-    accumulateLoad<3>(s, table, tableLane, acc);
+    const unsigned short* xt = reinterpret_cast<const unsigned short*>(xtile) + lane;
+    const unsigned quadRow = (lane & 3) * 8; // lane 4b+i reads row 4h+i of quad h
+    accumulateSlot<0>(s, xt, table, quadRow, acc);
+    accumulateSlot<1>(s, xt, table, quadRow, acc);
+    accumulateSlot<2>(s, xt, table, quadRow, acc);
+    accumulateSlot<3>(s, xt, table, quadRow, acc);
+    accumulateSlot<4>(s, xt, table, quadRow, acc);
+    accumulateSlot<5>(s, xt, table, quadRow, acc);
+    accumulateSlot<6>(s, xt, table, quadRow, acc);
+    accumulateSlot<7>(s, xt, table, quadRow, acc);
     __syncthreads();
 }
 
@@ -214,9 +200,9 @@ __device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, fl
 // instead of being copied; panel indices past the end repeat the last panel (harmless loads).
 template <unsigned G>
 __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& bounds,
-                                             unsigned lane, i32x4 xr, unsigned xLane,
-                                             float* table, unsigned tableLane,
-                                             f32x4 (&acc)[2][4]) {
+                                             unsigned lane, const std::int8_t* xSlice,
+                                             unsigned features, float* table, u32x4* xtile,
+                                             f32x4 (&acc)[2][2]) {
     const unsigned n = panelCount<G>(bounds);
     if (!n) return;
     unsigned p0 = nextPanel<G>(bounds, 0);
@@ -225,13 +211,13 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
     unsigned p2 = nextPanel<G>(bounds, p1 + 1);
     p2 = p2 == kEnd ? p1 : p2;
     Stage2 sa, sb;
-    loadStage2<G>(a, loadMeta(a, p0, lane), lane, xr, xLane, sa);
+    loadStage2<G>(a, loadMeta(a, p0, lane), lane, xSlice, features, sa);
     Meta m1 = loadMeta(a, p1, lane);
     Meta m2 = loadMeta(a, p2, lane);
 #pragma unroll 1
     for (unsigned i = 0; i < n; i += 2) {
         // Iteration i: stage 2 of panel i+1 (metadata m1), stage 1 of panel i+3, compute panel i.
-        loadStage2<G>(a, m1, lane, xr, xLane, sb);
+        loadStage2<G>(a, m1, lane, xSlice, features, sb);
         {
             unsigned p3 = nextPanel<G>(bounds, p2 + 1);
             p3 = p3 == kEnd ? p2 : p3;
@@ -239,9 +225,9 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
             m2 = loadMeta(a, p3, lane);
             p2 = p3;
         }
-        computeStage3(sa, lane, table, tableLane, acc);
+        computeStage3(sa, lane, table, xtile, acc);
         if (i + 1 >= n) break;
-        loadStage2<G>(a, m1, lane, xr, xLane, sa);
+        loadStage2<G>(a, m1, lane, xSlice, features, sa);
         {
             unsigned p3 = nextPanel<G>(bounds, p2 + 1);
             p3 = p3 == kEnd ? p2 : p3;
@@ -249,61 +235,51 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
             m2 = loadMeta(a, p3, lane);
             p2 = p3;
         }
-        computeStage3(sb, lane, table, tableLane, acc);
+        computeStage3(sb, lane, table, xtile, acc);
     }
 }
 
-// Sum the two halves' partial sums (even / odd slot positions) of one pass and store the 8 rows:
-// lanes of half 0 store rows 0..3 (quad 0), half 1 rows 4..7 (quad 1). Each lane holds features
-// 16t + {2m, 2m+8, 2m+1, 2m+9} (elements e = 0..3), stored as two float2.
-__device__ __forceinline__ void storeRows(f32x4 (&acc)[2][4], unsigned lane, float* base,
-                                          unsigned rowStride, unsigned validRows, unsigned colA,
+// Store the 8 rows of a pass: lane l holds features col and col + 8 (byte pair l) of rows
+// 4h + i (acc[h][0 / 1][i]).
+__device__ __forceinline__ void storeRows(const f32x4 (&acc)[2][2], float* base,
+                                          unsigned rowStride, unsigned validRows, unsigned col,
                                           bool nontemporal) {
 #pragma unroll
     for (unsigned h = 0; h < 2; ++h)
 #pragma unroll
-        for (unsigned e = 0; e < 4; ++e)
-#pragma unroll
-            for (unsigned i = 0; i < 4; ++i) acc[h][e][i] += __shfl_xor(acc[h][e][i], 32);
-    const unsigned h = lane >> 5;
-#pragma unroll
-    for (unsigned i = 0; i < 4; ++i) {
-        const unsigned row = h * 4 + i;
-        if (row >= validRows) continue;
-        float* r = base + std::size_t(row) * rowStride + colA;
-        const f32x2 lo = h ? f32x2{acc[1][0][i], acc[1][2][i]} : f32x2{acc[0][0][i], acc[0][2][i]};
-        const f32x2 hi = h ? f32x2{acc[1][1][i], acc[1][3][i]} : f32x2{acc[0][1][i], acc[0][3][i]};
-        if (nontemporal) {
-            __builtin_nontemporal_store(lo, reinterpret_cast<f32x2*>(r));
-            __builtin_nontemporal_store(hi, reinterpret_cast<f32x2*>(r + 8));
-        } else {
-            *reinterpret_cast<f32x2*>(r) = lo;
-            *reinterpret_cast<f32x2*>(r + 8) = hi;
+        for (unsigned i = 0; i < 4; ++i) {
+            const unsigned row = h * 4 + i;
+            if (row >= validRows) continue;
+            float* r = base + std::size_t(row) * rowStride + col;
+            if (nontemporal) {
+                __builtin_nontemporal_store(acc[h][0][i], r);
+                __builtin_nontemporal_store(acc[h][1][i], r + 8);
+            } else {
+                r[0] = acc[h][0][i];
+                r[8] = acc[h][1][i];
+            }
         }
-    }
 }
 
 template <unsigned G, unsigned Features>
 __device__ __forceinline__ void runGroup(const KernelArgs& a, const Sw32Task& task,
-                                         const Bounds& bounds, unsigned lane, i32x4 xr,
-                                         unsigned xLane, float* table, unsigned tableLane,
-                                         unsigned colA) {
+                                         const Bounds& bounds, unsigned lane,
+                                         const std::int8_t* xSlice, float* table, u32x4* xtile,
+                                         unsigned col) {
     const bool split = task.partial != kNoPartial;
     if (split && !((task.mask >> G) & 1u)) return;
-    f32x4 acc[2][4];
+    f32x4 acc[2][2];
 #pragma unroll
-    for (unsigned h = 0; h < 2; ++h)
-#pragma unroll
-        for (unsigned e = 0; e < 4; ++e) acc[h][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    rowGroupPass<G>(a, bounds, lane, xr, xLane, table, tableLane, acc);
+    for (unsigned h = 0; h < 2; ++h) acc[h][0] = acc[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rowGroupPass<G>(a, bounds, lane, xSlice, Features, table, xtile, acc);
     if (!split) {
         const unsigned row0 = task.sw * 32 + G * 8;
         if (row0 < a.rows)
-            storeRows(acc, lane, a.y + std::size_t(row0) * Features, Features,
-                      min(8u, a.rows - row0), colA, true);
+            storeRows(acc, a.y + std::size_t(row0) * Features, Features, min(8u, a.rows - row0),
+                      col, true);
     } else {
         const std::size_t tile = task.partial + __popc(task.mask & ((1u << G) - 1u));
-        storeRows(acc, lane, a.partials + tile * 8 * Features, Features, 8, colA, false);
+        storeRows(acc, a.partials + tile * 8 * Features, Features, 8, col, false);
     }
 }
 
@@ -319,6 +295,7 @@ template <unsigned Features>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void spmmInt8Kernel(
     KernelArgs a) {
     __shared__ __align__(16) float table[64];
+    __shared__ __align__(16) u32x4 xtile[64];
     __shared__ unsigned lastFlag;
     const unsigned lane = threadIdx.x;
     const unsigned slice = blockIdx.y;
@@ -335,26 +312,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void
         }
         bounds.lo[0] = bounds.hi[0] = 0;
     }
-    // X rows of this slice: base + src * Features, dword w of the 128-byte slice per lane.
-    i32x4 xr;
-    {
-        const std::uint64_t base = reinterpret_cast<std::uint64_t>(a.packedX) + slice * kSlice;
-        xr.x = int(unsigned(base));
-        xr.y = int((unsigned(base >> 32) & 0xFFFFu) | (Features << 16));
-        xr.z = int(a.cols);
-        xr.w = 0x00020000;
-    }
-    const unsigned w = lane & 31;
-    const unsigned xLane = 4 * w;
-    // Store column of element 0 (features 16t + 2m and 16t + 2m + 1; +8 for elements 1 and 3).
-    const unsigned colA = slice * kSlice + 16 * (w >> 2) + 2 * (w & 3);
-    // LDS table index of row (lane & 3) of the quad for the half's slot (load index added later).
-    const unsigned tableLane = (lane & 3) * 8 + 4 * (lane >> 5);
+    const std::int8_t* xSlice = a.packedX + slice * kSlice;
+    // Byte pair `lane` of the slice: features 16 * (lane / 8) + lane % 8 and + 8.
+    const unsigned col = slice * kSlice + 16 * (lane >> 3) + (lane & 7);
 
-    runGroup<0, Features>(a, task, bounds, lane, xr, xLane, table, tableLane, colA);
-    runGroup<1, Features>(a, task, bounds, lane, xr, xLane, table, tableLane, colA);
-    runGroup<2, Features>(a, task, bounds, lane, xr, xLane, table, tableLane, colA);
-    runGroup<3, Features>(a, task, bounds, lane, xr, xLane, table, tableLane, colA);
+    runGroup<0, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
+    runGroup<1, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
+    runGroup<2, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
+    runGroup<3, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
     if (task.partial == kNoPartial) return;
 
     // Completion ticket: the acq_rel RMW at agent scope publishes this task's partial tiles and,
@@ -413,6 +378,9 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
         throw std::runtime_error("launchSpmmInt8: invalid configuration argument (no tasks)");
     if (matrix.taskCount > 0x7FFFFFFFu)
         throw std::invalid_argument("launchSpmmInt8: too many tasks for one launch");
+    // 16-byte X tiles: the packed rows must start 16-byte aligned.
+    if (reinterpret_cast<std::uintptr_t>(packedX) % 16)
+        throw std::invalid_argument("launchSpmmInt8: packedX must be 16-byte aligned");
     const KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
                           rows,   cols};
     if (features == 128)
