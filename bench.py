@@ -11,8 +11,9 @@ Roofline: algorithmic bytes per launch B_alg = B_A + B_X + B_Y + B_P, computed f
   B_X = (F + 4) U                                                (each referenced X row + scale once)
   B_Y = 4 R F                                                    (Y written once)
   B_P = 64 F K                                                   (partial tiles written + read once)
-achieved = B_alg / kernel time, peak = 8.0e12 B/s. `traffic` (measured HBM bytes per launch) is read
-from profiles/counters_<workload>.json when a counter profile of this workload is present.
+achieved = B_alg / kernel time, peak = 8.0e12 B/s. `traffic` (HBM bytes per launch: rocprofv3
+FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a 1 GiB copy) is read from
+profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present.
 
 cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over a bounded prefix of
 SWs (~10 s of CPU work), extrapolated by SW count to one full SpMM.
@@ -174,7 +175,7 @@ def main() -> None:
         b = algorithmic_bytes(fmt, src, feats)
         achieved = b["B_alg"] / (ms * 1e-3)
         traffic = None
-        prof = ROOT / "profiles" / f"counters_{args.config}_f{feats}.json"
+        prof = ROOT / "profiles" / f"spmmInt8Kernel_{args.config}_f{feats}_counters.json"
         if prof.exists():
             traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
         results[feats] = {
