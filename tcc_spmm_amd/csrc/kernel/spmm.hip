@@ -5,7 +5,7 @@
 //   SW), slice = 128 features (blockIdx.y). The wave makes one pass per 8-row group (RW) g of the
 //   SW, visiting every panel of the task that touches g: the exclusive bucket of g and the shared
 //   buckets whose row-group mask contains g. A pass accumulates 8 rows x 128 features in
-//   32 FP32 registers per lane; at its end the rows are final (or a partial tile for split tasks).
+//   16 FP32 registers per lane; at its end the rows are final (or a partial tile for split tasks).
 //
 // Lane layout
 //   Per-slot data (metadata, scale, A table entries): lane L holds slot k = L & 7 and row
@@ -13,15 +13,20 @@
 //   X gathers: one dwordx4 load per panel, lane L fetching the 16-byte tile L & 7 of the 128-byte
 //   slice row of slot L >> 3 (eight rows per instruction). The tile is written to LDS and read back
 //   transposed: lane l then holds byte pair l (features 16(l/8) + l%8 and + 8) of all 8 slots.
-//   MFMA v_mfma_f32_4x4x1_16b_f32: A = the 4 row values of one quad of slot j (LDS table),
-//   B = the lane's dequantized feature, D = 4 rows x the lane's feature: acc[quad][feature].
+//   MFMA v_mfma_f32_4x4x4_16b_f16 (16 blocks of 4 x 4 x 4): lane 4b+i supplies A = row 4h+i of
+//   quad h for four slots (LDS table), lane 4b+j supplies B = its feature of the same four slots,
+//   and D[i][j] (row 4h+i, the lane's feature) lands in lane 4b+j register i: acc[quad][feature].
 //
-// Per panel: the A values of (slot k, row 8g + r) are TF32-rounded into an LDS table [8][8]
-// (zero where the slot does not touch the row); X bytes are sign-extended to FP32 (SDWA),
-// multiplied by the slot's scale (DPP broadcast) and TF32-rounded; TF32 x TF32 products are exact
-// in FP32, so any accumulation order reproduces the reference's products. The panels of a pass are
-// walked by a three-stage software pipeline (metadata two panels ahead; scales, A values and X one
-// panel ahead) whose memory operations are identical on every path.
+// Per panel: the A values of (slot k, row 8g + r) are TF32-rounded, scaled by 2^(e_k + kShift)
+// (e_k: binary exponent of slot k's scale) and stored as f16 in an LDS table [8][8]; X bytes are
+// sign-extended to FP32 (SDWA), multiplied by the mantissa of the slot's scale (DPP broadcast),
+// TF32-rounded and converted to f16 (exact: 11 significant bits in f16's normal range). The f16
+// products are exact in the FP32 accumulator and equal 2^kShift times the reference's TF32 x TF32
+// products, so any accumulation order reproduces them; a pass ends by scaling with 2^-kShift. A
+// panel whose scaled A values leave f16's normal range takes an FP32 path with the same products
+// (v_mfma_f32_4x4x1_16b_f32 on tf32(a) * 2^kShift and the TF32 features). The panels of a pass
+// are walked by a three-stage software pipeline (metadata two panels ahead; scales, A values and X
+// one panel ahead) whose memory operations are identical on every path.
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes an agent-scope acq_rel
@@ -42,6 +47,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __fp16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr unsigned kWave = 64;
 constexpr unsigned kSlice = 128;
@@ -144,55 +152,137 @@ __device__ __forceinline__ void loadStage2(const KernelArgs& a, const Meta& m, u
     s.x = *reinterpret_cast<const u32x4*>(xSlice + std::size_t(src) * features + 16 * (lane & 7));
 }
 
-// x_lo / x_hi of slot j = tf32(float(byte) * scale of slot j), for both bytes of the pair; the
-// scale comes from lane j of the lane's 16-lane row (DPP row broadcast). The s_nop covers the
-// VALU-write -> DPP-read hazard on the scale register.
-template <unsigned J>
-__device__ __forceinline__ void dequantPair(unsigned pair, float scale, float& lo, float& hi) {
-    float q0, q1;
-    asm volatile(
-        "v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "s_nop 1\n\t"
-        "v_mul_f32_dpp %0, %3, %0 row_newbcast:%4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %1, %3, %1 row_newbcast:%4 row_mask:0xf bank_mask:0xf"
-        : "=&v"(q0), "=&v"(q1)
-        : "v"(pair), "v"(scale), "i"(J));
-    lo = roundTf32(q0);
-    hi = roundTf32(q1);
+// Dequantization into f16 MFMA operands. With the slot's scale written s = m * 2^e (m in [0.5, 1)),
+// x_hat = tf32(fp32(q * s)) = tf32(fp32(q * m)) * 2^e exactly whenever s is normal, and
+// x~ = tf32(fp32(q * m)) lies in [0.5, 127]: eleven significant bits in f16's normal range, so f16
+// holds it exactly. The factor 2^e moves into the A operand: A' = tf32(a) * 2^(e + kShift), also
+// an 11-bit value, exact in f16 when it lies in f16's normal range. The MFMA then sums exact
+// products A' * x~ = 2^kShift * tf32(a) * x_hat in FP32, and the pass scales by 2^-kShift at the end.
+// TF32 rounding (ties away from zero) of the f32 product is "add half an ulp of the 11-bit
+// significand, then truncate": the truncation is the round-toward-zero f16 conversion.
+constexpr int kShift = 10;
+constexpr float kUnshift = 1.0f / 1024.0f;
+
+// X bytes in LDS: lane L (tile t = L & 7 of slot s = L >> 3) writes the 8 byte pairs of its tile to
+// rows p = 8t + i, column s, of a [64 pairs][8 slots] u16 array whose 8-row blocks are padded by
+// 16 bytes (row p at byte 144 (p / 8) + 16 (p % 8)), so the 64 lanes of each pair-i write hit 32
+// distinct banks. Lane l then reads row l — byte pair l of all 8 slots — with one 16-byte load:
+// dword m holds slot 2m (low half) and slot 2m + 1 (high half).
+constexpr unsigned kPairRowBlock = 144; // bytes per 8 rows of 16 bytes, plus padding
+
+// Dword M of the pair row: x_lo / x_hi of slots 2M and 2M + 1 = fp32(float(byte) * factor of the
+// slot), the factor of slot j coming from lane j of the lane's 16-lane row (DPP row broadcast).
+// The four conversions ahead of the first DPP read cover the VALU-write -> DPP-read hazard.
+template <unsigned M>
+__device__ __forceinline__ void scaleDword(unsigned d, float factor, float (&q)[4]) {
+    asm("v_cvt_f32_i32_sdwa %0, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_mul_f32_dpp %0, %5, %0 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %1, %5, %1 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %2, %5, %2 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %3, %5, %3 row_newbcast:%7 row_mask:0xf bank_mask:0xf"
+        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
+        : "v"(d), "v"(factor), "i"(2 * M), "i"(2 * M + 1));
 }
 
-template <unsigned J>
-__device__ __forceinline__ void accumulateSlot(const Stage2& s, const unsigned short* xt,
-                                               const float* table, unsigned quadRow,
-                                               f32x4 (&acc)[2][2]) {
-    float lo, hi;
-    dequantPair<J>(xt[J * 64], s.scale, lo, hi);
-    const float a0 = table[quadRow + J];      // rows 0..3 of the group (quad 0)
-    const float a1 = table[quadRow + 32 + J]; // rows 4..7 (quad 1)
-    acc[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, lo, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, hi, acc[0][1], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, lo, acc[1][0], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, hi, acc[1][1], 0, 0, 0);
+// Slots 4T..4T+3 as one K = 4 step of v_mfma_f32_4x4x4_16b_f16: B = the lane's feature of the four
+// slots (lo and hi byte of the pair), A = four slots of row 4h + (lane & 3) of the f16 table
+// (rows0 / rows1: that row of quad 0 / 1, all 8 slots).
+// Adding 0x1000 to the FP32 bits and converting toward zero is TF32 rounding (ties away).
+template <unsigned T>
+__device__ __forceinline__ void accumulateStepF16(const u32x4& pairs, float mant,
+                                                  const f16x8& rows0, const f16x8& rows1,
+                                                  f32x4 (&acc)[2][2]) {
+    float q0[4], q1[4];
+    scaleDword<2 * T>(pairs[2 * T], mant, q0);     // slots 4T, 4T+1: lo, hi, lo, hi
+    scaleDword<2 * T + 1>(pairs[2 * T + 1], mant, q1); // slots 4T+2, 4T+3
+#pragma unroll
+    for (unsigned j = 0; j < 4; ++j) {
+        q0[j] = __uint_as_float(__float_as_uint(q0[j]) + 0x1000u);
+        q1[j] = __uint_as_float(__float_as_uint(q1[j]) + 0x1000u);
+    }
+    const f16x2 l01 = __builtin_amdgcn_cvt_pkrtz(q0[0], q0[2]);
+    const f16x2 h01 = __builtin_amdgcn_cvt_pkrtz(q0[1], q0[3]);
+    const f16x2 l23 = __builtin_amdgcn_cvt_pkrtz(q1[0], q1[2]);
+    const f16x2 h23 = __builtin_amdgcn_cvt_pkrtz(q1[1], q1[3]);
+    const f16x4 bl = __builtin_bit_cast(f16x4, __builtin_shufflevector(l01, l23, 0, 1, 2, 3));
+    const f16x4 bh = __builtin_bit_cast(f16x4, __builtin_shufflevector(h01, h23, 0, 1, 2, 3));
+    const f16x4 a0 = __builtin_shufflevector(rows0, rows0, 4 * T, 4 * T + 1, 4 * T + 2, 4 * T + 3);
+    const f16x4 a1 = __builtin_shufflevector(rows1, rows1, 4 * T, 4 * T + 1, 4 * T + 2, 4 * T + 3);
+    acc[0][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a0, bl, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a0, bh, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a1, bl, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a1, bh, acc[1][1], 0, 0, 0);
 }
 
-__device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, float* table,
-                                              u32x4* xtile, f32x4 (&acc)[2][2]) {
-    // table[r][k] = tf32(A[row 8G + r][slot k]), 0 when absent; the X tiles go to LDS in row order
-    // and come back as byte pair `lane` of each slot row: xt[j * 64] = pair of slot j.
-    table[lane] = s.bits ? roundTf32(s.v) : 0.0f;
-    xtile[lane] = s.x;
-    __syncthreads();
-    const unsigned short* xt = reinterpret_cast<const unsigned short*>(xtile) + lane;
-    const unsigned quadRow = (lane & 3) * 8; // lane 4b+i reads row 4h+i of quad h
-    accumulateSlot<0>(s, xt, table, quadRow, acc);
-    accumulateSlot<1>(s, xt, table, quadRow, acc);
-    accumulateSlot<2>(s, xt, table, quadRow, acc);
-    accumulateSlot<3>(s, xt, table, quadRow, acc);
-    accumulateSlot<4>(s, xt, table, quadRow, acc);
-    accumulateSlot<5>(s, xt, table, quadRow, acc);
-    accumulateSlot<6>(s, xt, table, quadRow, acc);
-    accumulateSlot<7>(s, xt, table, quadRow, acc);
+// Slots 2M, 2M+1 on the exact FP32 path: x = tf32(float(byte) * scale of the slot), A from the FP32
+// table, one v_mfma_f32_4x4x1_16b_f32 per (slot, quad, feature).
+template <unsigned M>
+__device__ __forceinline__ void accumulateDwordF32(const u32x4& pairs, float scale,
+                                                   const float* table, unsigned quadRow,
+                                                   f32x4 (&acc)[2][2]) {
+    float q[4];
+    scaleDword<M>(pairs[M], scale, q);
+#pragma unroll
+    for (unsigned j = 0; j < 2; ++j) {
+        const float lo = roundTf32(q[2 * j]), hi = roundTf32(q[2 * j + 1]);
+        const float a0 = table[quadRow + 2 * M + j];      // rows 0..3 of the group (quad 0)
+        const float a1 = table[quadRow + 32 + 2 * M + j]; // rows 4..7 (quad 1)
+        acc[0][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, lo, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a0, hi, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, lo, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a1, hi, acc[1][1], 0, 0, 0);
+    }
+}
+
+struct Lds {
+    _Float16* table16;    // [8 rows][8 slots] A' values (f16 path)
+    float* table32;       // [8 rows][8 slots] tf32(a) * 2^kShift (FP32 path)
+    unsigned char* pairs; // X byte pairs, [64 pairs][8 slots] u16 with padded 8-row blocks
+};
+
+__device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, const Lds& lds,
+                                              f32x4 (&acc)[2][2]) {
+    // Lane L: slot k = L & 7, row r = (L >> 3) & 7; table index r * 8 + k = L.
+    const float at = s.bits ? roundTf32(s.v) : 0.0f;
+    const int e = __builtin_amdgcn_frexp_expf(s.scale);
+    const float mant = __builtin_amdgcn_frexp_mantf(s.scale);
+    const float ap = __builtin_amdgcn_ldexpf(at, e + kShift);
+    // f16 normal range [2^-14, 2^16): biased FP32 exponent 113..142. A subnormal scale (e < -125)
+    // breaks the exponent split and takes the FP32 path too.
+    const bool exact = at == 0.0f || (((__float_as_uint(ap) >> 23) & 0xFFu) - 113u <= 29u &&
+                                      e > -126);
+    {
+        unsigned short* w = reinterpret_cast<unsigned short*>(
+            lds.pairs + kPairRowBlock * (lane & 7) + 2 * (lane >> 3));
+#pragma unroll
+        for (unsigned i = 0; i < 8; ++i)
+            w[8 * i] = static_cast<unsigned short>(s.x[i / 2] >> (16 * (i & 1)));
+    }
+    if (__builtin_amdgcn_ballot_w64(!exact) == 0) {
+        lds.table16[lane] = static_cast<_Float16>(ap);
+        __syncthreads();
+        const u32x4 pairs = *reinterpret_cast<const u32x4*>(
+            lds.pairs + kPairRowBlock * (lane >> 3) + 16 * (lane & 7));
+        // A operands: row (lane & 3) of quad 0 and of quad 1, all 8 slots (16 bytes each).
+        const f16x8* table = reinterpret_cast<const f16x8*>(lds.table16);
+        const f16x8 rows0 = table[lane & 3], rows1 = table[4 + (lane & 3)];
+        accumulateStepF16<0>(pairs, mant, rows0, rows1, acc);
+        accumulateStepF16<1>(pairs, mant, rows0, rows1, acc);
+    } else {
+        // Some A' leaves f16's normal range (or a scale is subnormal): exact FP32 operands.
+        lds.table32[lane] = __builtin_amdgcn_ldexpf(at, kShift);
+        __syncthreads();
+        const u32x4 pairs = *reinterpret_cast<const u32x4*>(
+            lds.pairs + kPairRowBlock * (lane >> 3) + 16 * (lane & 7));
+        const unsigned quadRow = (lane & 3) * 8; // lane 4b+i reads row 4h+i of quad h
+        accumulateDwordF32<0>(pairs, s.scale, lds.table32, quadRow, acc);
+        accumulateDwordF32<1>(pairs, s.scale, lds.table32, quadRow, acc);
+        accumulateDwordF32<2>(pairs, s.scale, lds.table32, quadRow, acc);
+        accumulateDwordF32<3>(pairs, s.scale, lds.table32, quadRow, acc);
+    }
     __syncthreads();
 }
 
@@ -201,7 +291,7 @@ __device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, fl
 template <unsigned G>
 __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& bounds,
                                              unsigned lane, const std::int8_t* xSlice,
-                                             unsigned features, float* table, u32x4* xtile,
+                                             unsigned features, const Lds& lds,
                                              f32x4 (&acc)[2][2]) {
     const unsigned n = panelCount<G>(bounds);
     if (!n) return;
@@ -225,7 +315,7 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
             m2 = loadMeta(a, p3, lane);
             p2 = p3;
         }
-        computeStage3(sa, lane, table, xtile, acc);
+        computeStage3(sa, lane, lds, acc);
         if (i + 1 >= n) break;
         loadStage2<G>(a, m1, lane, xSlice, features, sa);
         {
@@ -235,7 +325,7 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
             m2 = loadMeta(a, p3, lane);
             p2 = p3;
         }
-        computeStage3(sb, lane, table, xtile, acc);
+        computeStage3(sb, lane, lds, acc);
     }
 }
 
@@ -264,14 +354,18 @@ __device__ __forceinline__ void storeRows(const f32x4 (&acc)[2][2], float* base,
 template <unsigned G, unsigned Features>
 __device__ __forceinline__ void runGroup(const KernelArgs& a, const Sw32Task& task,
                                          const Bounds& bounds, unsigned lane,
-                                         const std::int8_t* xSlice, float* table, u32x4* xtile,
-                                         unsigned col) {
+                                         const std::int8_t* xSlice, const Lds& lds, unsigned col) {
     const bool split = task.partial != kNoPartial;
     if (split && !((task.mask >> G) & 1u)) return;
     f32x4 acc[2][2];
 #pragma unroll
     for (unsigned h = 0; h < 2; ++h) acc[h][0] = acc[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    rowGroupPass<G>(a, bounds, lane, xSlice, Features, table, xtile, acc);
+    rowGroupPass<G>(a, bounds, lane, xSlice, Features, lds, acc);
+#pragma unroll
+    for (unsigned h = 0; h < 2; ++h) {
+        acc[h][0] *= kUnshift; // exact power-of-two scaling back to Y
+        acc[h][1] *= kUnshift;
+    }
     if (!split) {
         const unsigned row0 = task.sw * 32 + G * 8;
         if (row0 < a.rows)
@@ -294,8 +388,9 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
 template <unsigned Features>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void spmmInt8Kernel(
     KernelArgs a) {
-    __shared__ __align__(16) float table[64];
-    __shared__ __align__(16) u32x4 xtile[64];
+    __shared__ __align__(16) _Float16 table16[64];
+    __shared__ __align__(16) float table32[64];
+    __shared__ __align__(16) unsigned char pairs[8 * kPairRowBlock];
     __shared__ unsigned lastFlag;
     const unsigned lane = threadIdx.x;
     const unsigned slice = blockIdx.y;
@@ -316,10 +411,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void
     // Byte pair `lane` of the slice: features 16 * (lane / 8) + lane % 8 and + 8.
     const unsigned col = slice * kSlice + 16 * (lane >> 3) + (lane & 7);
 
-    runGroup<0, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
-    runGroup<1, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
-    runGroup<2, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
-    runGroup<3, Features>(a, task, bounds, lane, xSlice, table, xtile, col);
+    const Lds lds{table16, table32, pairs};
+    runGroup<0, Features>(a, task, bounds, lane, xSlice, lds, col);
+    runGroup<1, Features>(a, task, bounds, lane, xSlice, lds, col);
+    runGroup<2, Features>(a, task, bounds, lane, xSlice, lds, col);
+    runGroup<3, Features>(a, task, bounds, lane, xSlice, lds, col);
     if (task.partial == kNoPartial) return;
 
     // Completion ticket: the acq_rel RMW at agent scope publishes this task's partial tiles and,

@@ -199,3 +199,64 @@ def test_bad_feature_count_raises_before_launch(gpu):
     with pytest.raises(ValueError):
         launch_spmm_int8(dm.view, torch.zeros((64, 64), dtype=torch.int8, device=gpu),
                          torch.ones(64, device=gpu), y, 64, 64, 64)
+
+
+def _fallback_entries(csr, scales):
+    """Entries whose scaled f16 A operand tf32(a) * 2^(e + 10) (e: binary exponent of the source's
+    scale, scale = m * 2^e with m in [0.5, 1)) leaves f16's normal range, or whose scale is
+    subnormal: the panels holding them take the kernel's FP32 path."""
+    from test_oracle import tf32_exact
+    a = np.array([tf32_exact(float(v)) for v in csr.values])
+    _, e = np.frexp(scales.astype(np.float64)[csr.source_ids])
+    scaled = np.abs(np.ldexp(a, e + 10))
+    return ((scaled < 2.0 ** -14) | (scaled >= 2.0 ** 16)
+            | (scales[csr.source_ids] < np.float32(2.0 ** -126)))
+
+
+def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu):
+    """A values of 1e4, 1e-7 and 1e-30 and X rows scaled by 1e6, 1e-6 and into the subnormal range
+    push some panels onto the FP32 path; Y must still match the oracle (summation-conditioned
+    bound: the rows mix terms across 40 orders of magnitude)."""
+    base = T.synth_csr("t3000_24_11")
+    rng = np.random.default_rng(12)
+    val = base.values.copy()
+    pick = rng.random(val.size)
+    val[pick < 0.04] *= np.float32(1e4)
+    val[(pick >= 0.04) & (pick < 0.08)] *= np.float32(1e-7)
+    val[(pick >= 0.08) & (pick < 0.085)] *= np.float32(1e-30)
+    csr = T.make_canonical_csr(base.rows, base.cols, base.row_offsets, base.source_ids, val)
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, 128, seed=21, stddev=1.0)
+    rows = rng.permutation(csr.cols)
+    x[rows[:60]] *= np.float32(1e6)
+    x[rows[60:120]] *= np.float32(1e-6)
+    x[rows[120:125]] *= np.float32(1e-39)   # subnormal features -> subnormal scales
+    x[rows[125]] = 0.0
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    check_features(oracle, x, q, sc, pk)
+    flagged = _fallback_entries(csr, sc)
+    assert 0.01 < flagged.mean() < 0.5, flagged.mean()
+    _, y = _run(fmt, packed, scale, 128, gpu)
+    assert np.isfinite(y).all()
+    windows = np.arange(len(fmt.window_offsets) - 1, dtype=np.uint32)
+    _check_windows(oracle, csr, fmt, y, pk, sc, windows, "extreme", conditioned=True)
+
+
+def test_quantize_subnormal_and_huge_rows_bit_exact(oracle, gpu):
+    """Subnormal features (down to a scale of a few hundred denormal quanta) and features near the
+    top of the FP32 range quantize bit-exactly. Rows whose absmax / 127 underflows to zero
+    (absmax < 127 * 2^-150) are outside the contract: the reference then rounds +-inf or NaN with
+    lrintf, whose result C leaves unspecified."""
+    x = features(64, 128, seed=31, stddev=1.0)
+    x[1] *= np.float32(1e-39)      # subnormal inputs, subnormal scale
+    x[2] *= np.float32(1e-41)      # scale of about a hundred denormal quanta
+    x[3] *= np.float32(1e37)       # near the top of the FP32 range
+    x[4, :] = np.float32(3.0e38)
+    x[4, 1::2] = -np.float32(3.0e38)
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    q_ref, s_ref = oracle.quantize(x)
+    assert (s_ref > 0).all()
+    bad = [r for r in range(x.shape[0])
+           if sc[r].view(np.uint32) != s_ref[r].view(np.uint32) or not np.array_equal(q[r], q_ref[r])]
+    assert not bad, f"rows differing from the oracle: {bad}"
+    check_features(oracle, x, q, sc, pk)
