@@ -40,6 +40,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <stdexcept>
 
 namespace {
@@ -128,28 +129,90 @@ struct Stage2 {   // one panel, ready to compute
     u32x4 x;      // 16-byte tile L & 7 of the X row of slot L >> 3
 };
 
-__device__ __forceinline__ Meta loadMeta(const KernelArgs& a, unsigned panel, unsigned lane) {
-    const std::size_t first = std::size_t(panel) * 8;
-    const std::uint64_t md = __builtin_nontemporal_load(a.m.sourceMetadata + first + (lane & 7));
-    return {__builtin_nontemporal_load(a.m.sourceIds + first + (lane & 7)), unsigned(md),
-            unsigned(md >> 32), __builtin_nontemporal_load(a.m.sourceIds + first + (lane >> 3))};
-}
+// Memory access of one task. Narrow (every packed X slice and the scales addressable with 32-bit
+// byte offsets, the usual case): buffer loads. sourceIds and sourceMetadata use a per-task base
+// and a scalar panel offset; scales and X use buffers sized from `cols`, so the padding sentinel
+// source UINT32_MAX lands out of range and reads 0 without a clamp. Wide: 64-bit global loads
+// with clamped indices.
+constexpr int kNt = 2; // buffer cache policy: nontemporal (streamed once)
 
-template <unsigned G>
-__device__ __forceinline__ void loadStage2(const KernelArgs& a, const Meta& m, unsigned lane,
-                                           const std::int8_t* xSlice, unsigned features,
-                                           Stage2& s) {
-    const bool live = m.id < a.cols;
-    s.scale = a.scales[live ? m.id : 0u];
+template <bool Wide>
+struct Loader;
+
+template <>
+struct Loader<false> {
+    __amdgpu_buffer_rsrc_t ids, meta, scales, x;
+    const float* values;
+    unsigned first;     // task.begin: panel offsets are relative to it
+    unsigned xShift;    // log2(features)
+    unsigned sliceByte; // slice * 128
+
+    __device__ Loader(const KernelArgs& a, unsigned begin, unsigned features, unsigned slice)
+        : values(a.m.values), first(begin), xShift(features == 256 ? 8u : 7u),
+          sliceByte(slice * kSlice) {
+        const std::size_t slot0 = std::size_t(begin) * 8;
+        ids = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(a.m.sourceIds + slot0), 0,
+                                                0x7FFFFFF0, 0x00020000);
+        meta = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<std::uint64_t*>(a.m.sourceMetadata + slot0), 0, 0x7FFFFFF0, 0x00020000);
+        scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.scales), 0, a.cols * 4u,
+                                                   0x00020000);
+        x = __builtin_amdgcn_make_buffer_rsrc(const_cast<std::int8_t*>(a.packedX), 0,
+                                              a.cols << xShift, 0x00020000);
+    }
+    __device__ Meta meta8(unsigned panel, unsigned lane) const {
+        const int off = int((panel - first) * 32u);
+        const auto md = __builtin_amdgcn_raw_buffer_load_b64(meta, (lane & 7) * 8, 2 * off, kNt);
+        return {__builtin_amdgcn_raw_buffer_load_b32(ids, (lane & 7) * 4, off, kNt), md[0], md[1],
+                __builtin_amdgcn_raw_buffer_load_b32(ids, (lane >> 3) * 4, off, kNt)};
+    }
+    __device__ float scale(unsigned src) const {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(scales, src * 4u, 0, 0));
+    }
+    __device__ float value(unsigned idx) const { return __builtin_nontemporal_load(values + idx); }
+    __device__ u32x4 tile(unsigned src, unsigned lane) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(x, (src << xShift) + 16 * (lane & 7),
+                                                     int(sliceByte), 0);
+    }
+};
+
+template <>
+struct Loader<true> {
+    const KernelArgs* a;
+    const std::int8_t* xSlice;
+    unsigned features;
+
+    __device__ Loader(const KernelArgs& args, unsigned, unsigned f, unsigned slice)
+        : a(&args), xSlice(args.packedX + slice * kSlice), features(f) {}
+    __device__ Meta meta8(unsigned panel, unsigned lane) const {
+        const std::size_t first = std::size_t(panel) * 8;
+        const std::uint64_t md =
+            __builtin_nontemporal_load(a->m.sourceMetadata + first + (lane & 7));
+        return {__builtin_nontemporal_load(a->m.sourceIds + first + (lane & 7)), unsigned(md),
+                unsigned(md >> 32),
+                __builtin_nontemporal_load(a->m.sourceIds + first + (lane >> 3))};
+    }
+    __device__ float scale(unsigned src) const { return a->scales[min(src, a->cols - 1)]; }
+    __device__ float value(unsigned idx) const { return __builtin_nontemporal_load(a->m.values + idx); }
+    __device__ u32x4 tile(unsigned src, unsigned lane) const {
+        return *reinterpret_cast<const u32x4*>(xSlice + std::size_t(min(src, a->cols - 1)) * features +
+                                               16 * (lane & 7));
+    }
+};
+
+template <unsigned G, class Ld>
+__device__ __forceinline__ void loadStage2(const Ld& ld, const Meta& m, unsigned lane, Stage2& s) {
+    // Padding slots (source UINT32_MAX, metadata 0) have an empty row mask, so `present` needs no
+    // source check; their scale and X tile read 0 (narrow) or a clamped row (wide), both unused.
+    s.scale = ld.scale(m.id);
     const unsigned row = G * 8 + ((lane >> 3) & 7);
-    const bool present = live && ((m.mask >> row) & 1u);
+    const bool present = (m.mask >> row) & 1u;
     // The k-th set row bit of a slot owns values[base + k]; absent rows read values[base] (a valid
     // index: padding has base 0 and a matrix with panels has values).
     const unsigned idx = present ? m.base + __popc(m.mask & ((1u << row) - 1u)) : m.base;
-    s.v = __builtin_nontemporal_load(a.m.values + idx);
+    s.v = ld.value(idx);
     s.bits = present;
-    const unsigned src = m.gather < a.cols ? m.gather : 0u;
-    s.x = *reinterpret_cast<const u32x4*>(xSlice + std::size_t(src) * features + 16 * (lane & 7));
+    s.x = ld.tile(m.gather, lane);
 }
 
 // Dequantization into f16 MFMA operands. With the slot's scale written s = m * 2^e (m in [0.5, 1)),
@@ -187,10 +250,16 @@ __device__ __forceinline__ void scaleDword(unsigned d, float factor, float (&q)[
         : "v"(d), "v"(factor), "i"(2 * M), "i"(2 * M + 1));
 }
 
+// TF32-round two values and pack them as f16: adding 0x1000 to the FP32 pattern and converting
+// toward zero keeps eleven significant bits, rounded half away from zero.
+__device__ __forceinline__ f16x2 roundPack(float a, float b) {
+    return __builtin_amdgcn_cvt_pkrtz(__uint_as_float(__float_as_uint(a) + 0x1000u),
+                                      __uint_as_float(__float_as_uint(b) + 0x1000u));
+}
+
 // Slots 4T..4T+3 as one K = 4 step of v_mfma_f32_4x4x4_16b_f16: B = the lane's feature of the four
 // slots (lo and hi byte of the pair), A = four slots of row 4h + (lane & 3) of the f16 table
 // (rows0 / rows1: that row of quad 0 / 1, all 8 slots).
-// Adding 0x1000 to the FP32 bits and converting toward zero is TF32 rounding (ties away).
 template <unsigned T>
 __device__ __forceinline__ void accumulateStepF16(const u32x4& pairs, float mant,
                                                   const f16x8& rows0, const f16x8& rows1,
@@ -198,15 +267,10 @@ __device__ __forceinline__ void accumulateStepF16(const u32x4& pairs, float mant
     float q0[4], q1[4];
     scaleDword<2 * T>(pairs[2 * T], mant, q0);     // slots 4T, 4T+1: lo, hi, lo, hi
     scaleDword<2 * T + 1>(pairs[2 * T + 1], mant, q1); // slots 4T+2, 4T+3
-#pragma unroll
-    for (unsigned j = 0; j < 4; ++j) {
-        q0[j] = __uint_as_float(__float_as_uint(q0[j]) + 0x1000u);
-        q1[j] = __uint_as_float(__float_as_uint(q1[j]) + 0x1000u);
-    }
-    const f16x2 l01 = __builtin_amdgcn_cvt_pkrtz(q0[0], q0[2]);
-    const f16x2 h01 = __builtin_amdgcn_cvt_pkrtz(q0[1], q0[3]);
-    const f16x2 l23 = __builtin_amdgcn_cvt_pkrtz(q1[0], q1[2]);
-    const f16x2 h23 = __builtin_amdgcn_cvt_pkrtz(q1[1], q1[3]);
+    const f16x2 l01 = roundPack(q0[0], q0[2]);
+    const f16x2 h01 = roundPack(q0[1], q0[3]);
+    const f16x2 l23 = roundPack(q1[0], q1[2]);
+    const f16x2 h23 = roundPack(q1[1], q1[3]);
     const f16x4 bl = __builtin_bit_cast(f16x4, __builtin_shufflevector(l01, l23, 0, 1, 2, 3));
     const f16x4 bh = __builtin_bit_cast(f16x4, __builtin_shufflevector(h01, h23, 0, 1, 2, 3));
     const f16x4 a0 = __builtin_shufflevector(rows0, rows0, 4 * T, 4 * T + 1, 4 * T + 2, 4 * T + 3);
@@ -288,12 +352,11 @@ __device__ __forceinline__ void computeStage3(const Stage2& s, unsigned lane, co
 
 // One pass over the panels of row group G. Unrolled by two so the stage-2 buffers alternate
 // instead of being copied; panel indices past the end repeat the last panel (harmless loads).
-template <unsigned G>
-__device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& bounds,
-                                             unsigned lane, const std::int8_t* xSlice,
-                                             unsigned features, const Lds& lds,
-                                             f32x4 (&acc)[2][2]) {
-    const unsigned n = panelCount<G>(bounds);
+template <unsigned G, class Ld>
+__device__ __forceinline__ void rowGroupPass(const Ld& ld, const Bounds& bounds, unsigned lane,
+                                             const Lds& lds, f32x4 (&acc)[2][2]) {
+    // The panel count is uniform; keep the loop counter scalar.
+    const unsigned n = __builtin_amdgcn_readfirstlane(panelCount<G>(bounds));
     if (!n) return;
     unsigned p0 = nextPanel<G>(bounds, 0);
     unsigned p1 = nextPanel<G>(bounds, p0 + 1);
@@ -301,28 +364,28 @@ __device__ __forceinline__ void rowGroupPass(const KernelArgs& a, const Bounds& 
     unsigned p2 = nextPanel<G>(bounds, p1 + 1);
     p2 = p2 == kEnd ? p1 : p2;
     Stage2 sa, sb;
-    loadStage2<G>(a, loadMeta(a, p0, lane), lane, xSlice, features, sa);
-    Meta m1 = loadMeta(a, p1, lane);
-    Meta m2 = loadMeta(a, p2, lane);
+    loadStage2<G>(ld, ld.meta8(p0, lane), lane, sa);
+    Meta m1 = ld.meta8(p1, lane);
+    Meta m2 = ld.meta8(p2, lane);
 #pragma unroll 1
     for (unsigned i = 0; i < n; i += 2) {
         // Iteration i: stage 2 of panel i+1 (metadata m1), stage 1 of panel i+3, compute panel i.
-        loadStage2<G>(a, m1, lane, xSlice, features, sb);
+        loadStage2<G>(ld, m1, lane, sb);
         {
             unsigned p3 = nextPanel<G>(bounds, p2 + 1);
             p3 = p3 == kEnd ? p2 : p3;
             m1 = m2;
-            m2 = loadMeta(a, p3, lane);
+            m2 = ld.meta8(p3, lane);
             p2 = p3;
         }
         computeStage3(sa, lane, lds, acc);
         if (i + 1 >= n) break;
-        loadStage2<G>(a, m1, lane, xSlice, features, sa);
+        loadStage2<G>(ld, m1, lane, sa);
         {
             unsigned p3 = nextPanel<G>(bounds, p2 + 1);
             p3 = p3 == kEnd ? p2 : p3;
             m1 = m2;
-            m2 = loadMeta(a, p3, lane);
+            m2 = ld.meta8(p3, lane);
             p2 = p3;
         }
         computeStage3(sb, lane, lds, acc);
@@ -351,16 +414,16 @@ __device__ __forceinline__ void storeRows(const f32x4 (&acc)[2][2], float* base,
         }
 }
 
-template <unsigned G, unsigned Features>
-__device__ __forceinline__ void runGroup(const KernelArgs& a, const Sw32Task& task,
-                                         const Bounds& bounds, unsigned lane,
-                                         const std::int8_t* xSlice, const Lds& lds, unsigned col) {
+template <unsigned G, unsigned Features, class Ld>
+__device__ __forceinline__ void runGroup(const KernelArgs& a, const Ld& ld, const Sw32Task& task,
+                                         const Bounds& bounds, unsigned lane, const Lds& lds,
+                                         unsigned col) {
     const bool split = task.partial != kNoPartial;
     if (split && !((task.mask >> G) & 1u)) return;
     f32x4 acc[2][2];
 #pragma unroll
     for (unsigned h = 0; h < 2; ++h) acc[h][0] = acc[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    rowGroupPass<G>(a, bounds, lane, xSlice, Features, lds, acc);
+    rowGroupPass<G>(ld, bounds, lane, lds, acc);
 #pragma unroll
     for (unsigned h = 0; h < 2; ++h) {
         acc[h][0] *= kUnshift; // exact power-of-two scaling back to Y
@@ -385,7 +448,7 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
     return xcd * q + min(xcd, r) + j;
 }
 
-template <unsigned Features>
+template <unsigned Features, bool Wide>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void spmmInt8Kernel(
     KernelArgs a) {
     __shared__ __align__(16) _Float16 table16[64];
@@ -407,15 +470,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void
         }
         bounds.lo[0] = bounds.hi[0] = 0;
     }
-    const std::int8_t* xSlice = a.packedX + slice * kSlice;
+    const Loader<Wide> ld(a, task.begin, Features, slice);
     // Byte pair `lane` of the slice: features 16 * (lane / 8) + lane % 8 and + 8.
     const unsigned col = slice * kSlice + 16 * (lane >> 3) + (lane & 7);
 
     const Lds lds{table16, table32, pairs};
-    runGroup<0, Features>(a, task, bounds, lane, xSlice, lds, col);
-    runGroup<1, Features>(a, task, bounds, lane, xSlice, lds, col);
-    runGroup<2, Features>(a, task, bounds, lane, xSlice, lds, col);
-    runGroup<3, Features>(a, task, bounds, lane, xSlice, lds, col);
+    runGroup<0, Features>(a, ld, task, bounds, lane, lds, col);
+    runGroup<1, Features>(a, ld, task, bounds, lane, lds, col);
+    runGroup<2, Features>(a, ld, task, bounds, lane, lds, col);
+    runGroup<3, Features>(a, ld, task, bounds, lane, lds, col);
     if (task.partial == kNoPartial) return;
 
     // Completion ticket: the acq_rel RMW at agent scope publishes this task's partial tiles and,
@@ -460,7 +523,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4))) void
 template <unsigned Features>
 void launch(const KernelArgs& args, hipStream_t stream) {
     const dim3 grid(args.m.taskCount, Features / kSlice);
-    hipLaunchKernelGGL(spmmInt8Kernel<Features>, grid, dim3(kWave), 0, stream, args);
+    // Buffer addressing needs the packed X and the scales within 32-bit byte offsets, with room for
+    // the padding sentinel to land out of range.
+    // TCC_SPMM_FORCE_WIDE selects the 64-bit instance for any size (used by the tests).
+    const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull ||
+                      std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
+    if (wide)
+        hipLaunchKernelGGL((spmmInt8Kernel<Features, true>), grid, dim3(kWave), 0, stream, args);
+    else
+        hipLaunchKernelGGL((spmmInt8Kernel<Features, false>), grid, dim3(kWave), 0, stream, args);
 }
 
 } // namespace

@@ -260,3 +260,24 @@ def test_quantize_subnormal_and_huge_rows_bit_exact(oracle, gpu):
            if sc[r].view(np.uint32) != s_ref[r].view(np.uint32) or not np.array_equal(q[r], q_ref[r])]
     assert not bad, f"rows differing from the oracle: {bad}"
     check_features(oracle, x, q, sc, pk)
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
+    """The 64-bit-addressing kernel instance (taken when packed X exceeds 32-bit byte offsets) gives
+    the same Y as the buffer-addressed one."""
+    for case in ("single", "tail_33", "all_masks", "long_shared", "panels_385", "split_mixed",
+                 "split_two", "random_3"):
+        rows, cols = (int(x) for x in golden[f"{case}/dims"])
+        off, src, val = (golden[f"{case}/csr_offsets"], golden[f"{case}/csr_sources"],
+                         golden[f"{case}/csr_values"])
+        fmt = T.convert_csr_to_sw32(rows, cols, T.make_canonical_csr(rows, cols, off, src, val))
+        x = features(cols, feats, seed=rows + 3 * cols, stddev=2.0)
+        packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+        _, y_narrow = _run(fmt, packed, scale, feats, gpu)
+        monkeypatch.setenv("TCC_SPMM_FORCE_WIDE", "1")
+        _, y_wide = _run(fmt, packed, scale, feats, gpu)
+        monkeypatch.delenv("TCC_SPMM_FORCE_WIDE")
+        assert np.array_equal(y_wide.view(np.uint32), y_narrow.view(np.uint32)), case
+        y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
+        assert_close(y_wide, y_ref, f"{case} F{feats} wide")
