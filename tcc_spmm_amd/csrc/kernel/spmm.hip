@@ -396,7 +396,9 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, const TaskWalk& w, unsi
     unsigned ga = groupsAt(lo);
     loadStage<G>(ld, ld.meta8(lo, lane), ga, lane, sa);
     unsigned g1 = groupsAt(p1), g2 = groupsAt(p2), gb = 0;
+    // The loop expects m1's loads to be older than m2's (waits are counted in issue order).
     Meta m1 = ld.meta8(p1, lane);
+    __builtin_amdgcn_sched_barrier(0);
     Meta m2 = ld.meta8(p2, lane);
     unsigned p = p2;
     const unsigned pairs = n / 2;
@@ -410,6 +412,9 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, const TaskWalk& w, unsi
         g1 = g2;
         g2 = groupsAt(p);
         m2 = ld.meta8(p, lane);
+        // Issue this half's loads before any use of the previous half's: the vmcnt counter is in
+        // order, so computing first would wait for loads issued only half an iteration ago.
+        __builtin_amdgcn_sched_barrier(0);
         flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G>(sa, ga, lane, w.lds, acc));
         ga = g1;
         loadStage<G>(ld, m1, ga, lane, sa);
@@ -418,6 +423,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, const TaskWalk& w, unsi
         g1 = g2;
         g2 = groupsAt(p);
         m2 = ld.meta8(p, lane);
+        __builtin_amdgcn_sched_barrier(0);
         flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G>(sb, gb, lane, w.lds, acc));
     }
     if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G>(sa, ga, lane, w.lds, acc));
