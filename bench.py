@@ -71,6 +71,34 @@ def time_launches(dm, packed, scale, y, steps, warmup, stream):
     return start.elapsed_time(end) / steps
 
 
+def time_feature_prep(x, xq, scale, packed, stream, reps=5):
+    """quantizeFeaturesInt8 and packFeaturesInt8x16 on resident buffers: ms per call (median of `reps`
+    event-timed calls on `stream`) and HBM-roofline fraction of their algorithmic bytes."""
+    import torch
+    from tcc_spmm_amd.device import pack_features_int8x16, quantize_features_int8
+    out = {}
+    sources, features = x.shape
+    for name, fn, nbytes in (
+            ("quantize", lambda: quantize_features_int8(x, xq, scale, stream=stream),
+             sources * (4 * features + features + 4)),
+            ("pack", lambda: pack_features_int8x16(xq, packed, stream=stream),
+             2 * sources * features)):
+        fn()
+        times = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            fn()
+            end.record(stream)
+            end.synchronize()
+            times.append(start.elapsed_time(end))
+        ms = float(np.median(times))
+        out[name] = {"ms": round(ms, 4), "bytes": int(nbytes),
+                     "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+    return out
+
+
 def run_workload(csr, fmt, features, seed, steps, warmup, dev):
     import torch
     import tcc_spmm_amd as T
@@ -78,10 +106,12 @@ def run_workload(csr, fmt, features, seed, steps, warmup, dev):
 
     t0 = time.time()
     x = T.synth_features(csr.cols, features, seed)
-    xq, scale = quantize_features_int8(torch.from_numpy(x).to(dev))
+    xd = torch.from_numpy(x).to(dev)
     del x
+    xq, scale = quantize_features_int8(xd)
     packed = pack_features_int8x16(xq)
-    del xq
+    prep = time_feature_prep(xd, xq, scale, packed, torch.cuda.Stream())
+    del xd, xq
     dm = TorchDeviceMatrix(fmt, features, device=dev)
     y = torch.empty((csr.rows, features), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
@@ -95,7 +125,7 @@ def run_workload(csr, fmt, features, seed, steps, warmup, dev):
     y0 = y[0, :8].cpu().numpy().tolist()
     del dm, y, packed, scale
     torch.cuda.empty_cache()
-    return ms, means, y0
+    return ms, means, y0, prep
 
 
 def cpu_baseline(csr, fmt, features, seed, budget_s=10.0):
@@ -171,7 +201,7 @@ def main() -> None:
     for feats, seed in ((128, 103), (256, 104)):
         if feats == 256 and args.no_f256:
             continue
-        ms, means, y0 = run_workload(csr, fmt, feats, seed, args.steps, args.warmup, dev)
+        ms, means, y0, prep = run_workload(csr, fmt, feats, seed, args.steps, args.warmup, dev)
         b = algorithmic_bytes(fmt, src, feats)
         achieved = b["B_alg"] / (ms * 1e-3)
         traffic = None
@@ -179,7 +209,7 @@ def main() -> None:
         if prof.exists():
             traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
         results[feats] = {
-            "ms": round(ms, 4), "means_ms": [round(m, 4) for m in means],
+            "ms": round(ms, 4), "means_ms": [round(m, 4) for m in means], "feature_prep": prep,
             "gbps": round(achieved / 1e9, 1), "bytes": b, "y00_07": y0,
             "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1),
                          "peak": HBM_PEAK / 1e9, "unit": "GB/s",
@@ -204,7 +234,8 @@ def main() -> None:
                    "tasks": stats["tasks"], "split_sw": stats["split_sw"],
                    "partial_count": stats["partial_count"], "panels": stats["panels"]},
         "gbps": r["gbps"], "roofline": r["roofline"], "cpu_baseline": base,
-        "f256": results.get(256), "f128_detail": {k: r[k] for k in ("means_ms", "bytes", "y00_07")},
+        "f256": results.get(256),
+        "f128_detail": {k: r[k] for k in ("means_ms", "bytes", "y00_07", "feature_prep")},
     }
     print(json.dumps(line), flush=True)
 

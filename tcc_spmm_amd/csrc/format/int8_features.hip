@@ -1,9 +1,10 @@
 // Per-source INT8 quantization and packed16 byte permutation for gfx950 (wave64).
 //
-// quantize: one wave per source row (4 rows per 256-thread workgroup). Lanes stride the row with
-// coalesced loads, the row's |x| maximum is reduced across the wave with DPP-backed shuffles, and
-// every element is divided by the scale with the IEEE-correct FP32 divide and rounded half-to-even.
-// Results are bit-identical to reference src/format/int8_quantize.cu:4-25.
+// quantize: rows of features % 4 == 0 use quantizeRows4 (F/4 lanes per row up to 64, 16-byte loads,
+// one dword store per 4 quantized bytes); other rows one wave per row (quantizeRows). The row's |x|
+// maximum is reduced across its lanes with shuffles, and every element is divided by the scale with
+// the IEEE-correct FP32 divide and rounded half-to-even. Results are bit-identical to reference
+// src/format/int8_quantize.cu:4-25.
 //
 // pack: one thread per 16-byte tile; four v_perm_b32 byte shuffles turn q[0..15] into
 // [q0,q8,q1,q9,...,q7,q15] (reference src/format/pack_int8.cu:6-15). Unaligned buffers use a
@@ -41,6 +42,44 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
     }
 }
 
+// Vector path for features % 4 == 0 with 16-byte aligned rows: `Lanes` (a power of two <= 64) lanes
+// per row, each loading 16-byte groups of 4 features and storing their 4 quantized bytes as one
+// dword; a wave holds 64 / Lanes rows. Same arithmetic as quantizeRows (IEEE divide, round half to
+// even, clamp).
+__device__ __forceinline__ int quantizeOne(float v, float s) {
+    const int r = __float2int_rn(v / s);
+    return r < -127 ? -127 : (r > 127 ? 127 : r);
+}
+
+template <unsigned Lanes>
+__global__ __launch_bounds__(256) void quantizeRows4(const float4* __restrict__ x,
+                                                      unsigned* __restrict__ q,
+                                                      float* __restrict__ scale, unsigned sources,
+                                                      unsigned groups) {
+    const unsigned lane = threadIdx.x & (Lanes - 1);
+    const std::size_t row = (std::size_t(blockIdx.x) * 256 + threadIdx.x) / Lanes;
+    const bool live = row < sources;
+    const float4* xr = x + std::size_t(live ? row : 0) * groups;
+    float m = 0.0f;
+    for (unsigned j = lane; j < groups; j += Lanes) {
+        const float4 v = xr[j];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (unsigned offset = Lanes / 2; offset > 0; offset >>= 1)
+        m = fmaxf(m, __shfl_xor(m, offset));
+    if (!live) return;
+    const float s = m == 0.0f ? 1.0f : m / 127.0f;
+    if (lane == 0) scale[row] = s;
+    unsigned* qr = q + std::size_t(row) * groups;
+    for (unsigned j = lane; j < groups; j += Lanes) {
+        const float4 v = xr[j];
+        qr[j] = (unsigned(quantizeOne(v.x, s)) & 0xFFu) | (unsigned(quantizeOne(v.y, s)) & 0xFFu) << 8 |
+                (unsigned(quantizeOne(v.z, s)) & 0xFFu) << 16 |
+                (unsigned(quantizeOne(v.w, s)) & 0xFFu) << 24;
+    }
+}
+
 __global__ __launch_bounds__(256) void packTiles(const uint4* __restrict__ q,
                                                  uint4* __restrict__ out, std::size_t tiles) {
     const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -70,9 +109,32 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
                           std::uint32_t features, hipStream_t stream) {
     // A zero-sized grid is a launch error, reported like the runtime would (std::runtime_error).
     if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
-    const unsigned blocks = (sources + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipLaunchKernelGGL(quantizeRows, dim3(blocks), dim3(kWave * kRowsPerBlock), 0, stream, x, q,
-                       scale, sources, features);
+    const bool vector = features % 4 == 0 && reinterpret_cast<std::uintptr_t>(x) % 16 == 0 &&
+                        reinterpret_cast<std::uintptr_t>(q) % 4 == 0;
+    if (vector) {
+        const unsigned groups = features / 4;
+        unsigned lanes = 1;
+        while (lanes < groups && lanes < kWave) lanes *= 2;
+        const std::size_t threads = std::size_t(sources) * lanes;
+        const std::size_t blocks64 = (threads + 255) / 256;
+        if (blocks64 > 0xFFFFFFFFull) throw std::invalid_argument("quantize: too many rows");
+        const unsigned blocks = unsigned(blocks64);
+        const auto* xv = reinterpret_cast<const float4*>(x);
+        auto* qv = reinterpret_cast<unsigned*>(q);
+        switch (lanes) {
+        case 1: hipLaunchKernelGGL(quantizeRows4<1>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        case 2: hipLaunchKernelGGL(quantizeRows4<2>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        case 4: hipLaunchKernelGGL(quantizeRows4<4>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        case 8: hipLaunchKernelGGL(quantizeRows4<8>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        case 16: hipLaunchKernelGGL(quantizeRows4<16>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        case 32: hipLaunchKernelGGL(quantizeRows4<32>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        default: hipLaunchKernelGGL(quantizeRows4<64>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        }
+    } else {
+        const unsigned blocks = (sources + kRowsPerBlock - 1) / kRowsPerBlock;
+        hipLaunchKernelGGL(quantizeRows, dim3(blocks), dim3(kWave * kRowsPerBlock), 0, stream, x,
+                           q, scale, sources, features);
+    }
     checkHip(hipGetLastError());
 }
 

@@ -281,3 +281,22 @@ def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
         assert np.array_equal(y_wide.view(np.uint32), y_narrow.view(np.uint32)), case
         y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
         assert_close(y_wide, y_ref, f"{case} F{feats} wide")
+
+
+@pytest.mark.parametrize("shape,offset", [((33, 18), 0), ((20, 5), 0), ((40, 64), 1), ((3, 2052), 0)])
+def test_quantize_scalar_and_vector_paths_bit_exact(oracle, gpu, shape, offset):
+    """Widths that are not a multiple of 4 and inputs that are not 16-byte aligned take the one-wave-
+    per-row kernel; 2052 features take the vector kernel with several groups per lane."""
+    import torch
+    from tcc_spmm_amd.device import quantize_features_int8
+    s, f = shape
+    x = features(s, f, seed=s * 31 + f, stddev=2.0, outlier_fraction=0.1, outlier_scale=50.0)
+    x[0] = 0.0
+    flat = torch.zeros(s * f + offset, dtype=torch.float32, device=gpu)
+    flat[offset:] = torch.from_numpy(x.ravel()).to(gpu)
+    xs = flat[offset:].view(s, f)
+    q, scale = quantize_features_int8(xs)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize(x)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
