@@ -1,9 +1,10 @@
 // Per-source INT8 quantization and packed16 byte permutation for gfx950 (wave64).
 //
-// quantize: rows of features % 4 == 0 use quantizeRows4 (F/4 lanes per row up to 64, 16-byte loads,
-// one dword store per 4 quantized bytes); other rows one wave per row (quantizeRows). The row's |x|
-// maximum is reduced across its lanes with shuffles, and every element is divided by the scale with
-// the IEEE-correct FP32 divide and rounded half-to-even. Results are bit-identical to reference
+// quantize: rows of features % 4 == 0 (16-byte aligned) use 16-byte loads of 4-feature groups and one
+// dword store per 4 quantized bytes: quantizeRowsFit for F <= 256 (one group per lane, several rows
+// per thread held in registers, X read once), quantizeRowsLong above; other rows one wave per row
+// (quantizeRows). The row's |x| maximum is reduced across its lanes with shuffles, and every element
+// is divided by the scale with the IEEE-correct FP32 divide and rounded half-to-even. Results are bit-identical to reference
 // src/format/int8_quantize.cu:4-25.
 //
 // pack: one thread per 16-byte tile; four v_perm_b32 byte shuffles turn q[0..15] into
@@ -42,42 +43,80 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
     }
 }
 
-// Vector path for features % 4 == 0 with 16-byte aligned rows: `Lanes` (a power of two <= 64) lanes
-// per row, each loading 16-byte groups of 4 features and storing their 4 quantized bytes as one
-// dword; a wave holds 64 / Lanes rows. Same arithmetic as quantizeRows (IEEE divide, round half to
-// even, clamp).
+// Vector paths for features % 4 == 0 with 16-byte aligned rows. Same arithmetic as quantizeRows
+// (IEEE divide, round half to even, clamp).
 __device__ __forceinline__ int quantizeOne(float v, float s) {
     const int r = __float2int_rn(v / s);
     return r < -127 ? -127 : (r > 127 ? 127 : r);
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned quantizeGroup(f32x4 v, float s) {
+    return (unsigned(quantizeOne(v.x, s)) & 0xFFu) | (unsigned(quantizeOne(v.y, s)) & 0xFFu) << 8 |
+           (unsigned(quantizeOne(v.z, s)) & 0xFFu) << 16 | (unsigned(quantizeOne(v.w, s)) & 0xFFu) << 24;
+}
+
+__device__ __forceinline__ float absMax(f32x4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Rows of at most 64 groups of 4 features (F <= 256): `Lanes` (a power of two >= groups) lanes per
+// row, each holding one group; a thread handles kQuantRows rows kRowsPerPass apart, issuing all of
+// its 16-byte loads before the reductions, so a wave keeps 4 KiB of X in flight and reads X once.
+// X is streamed with nontemporal loads and q with nontemporal stores (neither is re-read here).
+constexpr unsigned kQuantRows = 4;
+
 template <unsigned Lanes>
-__global__ __launch_bounds__(256) void quantizeRows4(const float4* __restrict__ x,
-                                                      unsigned* __restrict__ q,
-                                                      float* __restrict__ scale, unsigned sources,
-                                                      unsigned groups) {
+__global__ __launch_bounds__(256) void quantizeRowsFit(const f32x4* __restrict__ x,
+                                                        unsigned* __restrict__ q,
+                                                        float* __restrict__ scale,
+                                                        unsigned sources, unsigned groups) {
+    constexpr unsigned kRowsPerPass = 256 / Lanes;
     const unsigned lane = threadIdx.x & (Lanes - 1);
-    const std::size_t row = (std::size_t(blockIdx.x) * 256 + threadIdx.x) / Lanes;
-    const bool live = row < sources;
-    const float4* xr = x + std::size_t(live ? row : 0) * groups;
-    float m = 0.0f;
-    for (unsigned j = lane; j < groups; j += Lanes) {
-        const float4 v = xr[j];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const std::size_t row0 = std::size_t(blockIdx.x) * kRowsPerPass * kQuantRows + threadIdx.x / Lanes;
+    f32x4 v[kQuantRows];
+    float m[kQuantRows];
+#pragma unroll
+    for (unsigned r = 0; r < kQuantRows; ++r) {
+        const std::size_t row = row0 + r * kRowsPerPass;
+        const bool live = row < sources && lane < groups;
+        v[r] = __builtin_nontemporal_load(x + (live ? row * groups + lane : 0));
+        if (!live) v[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        m[r] = absMax(v[r]);
     }
 #pragma unroll
     for (unsigned offset = Lanes / 2; offset > 0; offset >>= 1)
-        m = fmaxf(m, __shfl_xor(m, offset));
-    if (!live) return;
+#pragma unroll
+        for (unsigned r = 0; r < kQuantRows; ++r) m[r] = fmaxf(m[r], __shfl_xor(m[r], offset));
+#pragma unroll
+    for (unsigned r = 0; r < kQuantRows; ++r) {
+        const std::size_t row = row0 + r * kRowsPerPass;
+        if (row >= sources) break;
+        const float s = m[r] == 0.0f ? 1.0f : m[r] / 127.0f;
+        if (lane == 0) scale[row] = s;
+        if (lane < groups) __builtin_nontemporal_store(quantizeGroup(v[r], s), q + row * groups + lane);
+    }
+}
+
+// Rows of more than 64 groups: one wave per row, looping over the groups twice (maximum, then
+// quantize; the second read of the row hits L2).
+__global__ __launch_bounds__(256) void quantizeRowsLong(const f32x4* __restrict__ x,
+                                                         unsigned* __restrict__ q,
+                                                         float* __restrict__ scale,
+                                                         unsigned sources, unsigned groups) {
+    const unsigned lane = threadIdx.x & (kWave - 1);
+    const std::size_t row = (std::size_t(blockIdx.x) * 256 + threadIdx.x) / kWave;
+    if (row >= sources) return;
+    const f32x4* xr = x + row * groups;
+    float m = 0.0f;
+    for (unsigned j = lane; j < groups; j += kWave) m = fmaxf(m, absMax(xr[j]));
+#pragma unroll
+    for (unsigned offset = kWave / 2; offset > 0; offset >>= 1) m = fmaxf(m, __shfl_xor(m, offset));
     const float s = m == 0.0f ? 1.0f : m / 127.0f;
     if (lane == 0) scale[row] = s;
-    unsigned* qr = q + std::size_t(row) * groups;
-    for (unsigned j = lane; j < groups; j += Lanes) {
-        const float4 v = xr[j];
-        qr[j] = (unsigned(quantizeOne(v.x, s)) & 0xFFu) | (unsigned(quantizeOne(v.y, s)) & 0xFFu) << 8 |
-                (unsigned(quantizeOne(v.z, s)) & 0xFFu) << 16 |
-                (unsigned(quantizeOne(v.w, s)) & 0xFFu) << 24;
-    }
+    unsigned* qr = q + row * groups;
+    for (unsigned j = lane; j < groups; j += kWave) qr[j] = quantizeGroup(xr[j], s);
 }
 
 __global__ __launch_bounds__(256) void packTiles(const uint4* __restrict__ q,
@@ -113,22 +152,27 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
                         reinterpret_cast<std::uintptr_t>(q) % 4 == 0;
     if (vector) {
         const unsigned groups = features / 4;
-        unsigned lanes = 1;
-        while (lanes < groups && lanes < kWave) lanes *= 2;
-        const std::size_t threads = std::size_t(sources) * lanes;
-        const std::size_t blocks64 = (threads + 255) / 256;
-        if (blocks64 > 0xFFFFFFFFull) throw std::invalid_argument("quantize: too many rows");
-        const unsigned blocks = unsigned(blocks64);
-        const auto* xv = reinterpret_cast<const float4*>(x);
+        const auto* xv = reinterpret_cast<const f32x4*>(x);
         auto* qv = reinterpret_cast<unsigned*>(q);
-        switch (lanes) {
-        case 1: hipLaunchKernelGGL(quantizeRows4<1>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        case 2: hipLaunchKernelGGL(quantizeRows4<2>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        case 4: hipLaunchKernelGGL(quantizeRows4<4>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        case 8: hipLaunchKernelGGL(quantizeRows4<8>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        case 16: hipLaunchKernelGGL(quantizeRows4<16>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        case 32: hipLaunchKernelGGL(quantizeRows4<32>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
-        default: hipLaunchKernelGGL(quantizeRows4<64>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale, sources, groups); break;
+        if (groups > kWave) {
+            const unsigned blocks = unsigned((std::size_t(sources) * kWave + 255) / 256);
+            hipLaunchKernelGGL(quantizeRowsLong, dim3(blocks), dim3(256), 0, stream, xv, qv, scale,
+                               sources, groups);
+        } else {
+            unsigned lanes = 1;
+            while (lanes < groups) lanes *= 2;
+            const std::size_t rowsPerBlock = std::size_t(256 / lanes) * kQuantRows;
+            const unsigned blocks = unsigned((sources + rowsPerBlock - 1) / rowsPerBlock);
+            switch (lanes) {
+#define TCC_QUANT_CASE(L)                                                                          \
+    case L:                                                                                        \
+        hipLaunchKernelGGL(quantizeRowsFit<L>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale,  \
+                           sources, groups);                                                       \
+        break;
+                TCC_QUANT_CASE(1) TCC_QUANT_CASE(2) TCC_QUANT_CASE(4) TCC_QUANT_CASE(8)
+                TCC_QUANT_CASE(16) TCC_QUANT_CASE(32) TCC_QUANT_CASE(64)
+#undef TCC_QUANT_CASE
+            }
         }
     } else {
         const unsigned blocks = (sources + kRowsPerBlock - 1) / kRowsPerBlock;

@@ -283,10 +283,17 @@ def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
         assert_close(y_wide, y_ref, f"{case} F{feats} wide")
 
 
-@pytest.mark.parametrize("shape,offset", [((33, 18), 0), ((20, 5), 0), ((40, 64), 1), ((3, 2052), 0)])
+@pytest.mark.parametrize("shape,offset", [
+    ((33, 18), 0), ((20, 5), 0), ((40, 64), 1),            # scalar kernel: F % 4 != 0, misaligned
+    ((3, 2052), 0), ((70, 260), 0),                         # long-row kernel: > 64 groups per row
+    ((1, 4), 0), ((1029, 4), 0), ((515, 12), 0),            # fit kernel, 1 and 4 lanes (3 live)
+    ((257, 100), 0), ((131, 128), 0), ((67, 256), 0),       # fit kernel, 32 and 64 lanes, ragged tail
+])
 def test_quantize_scalar_and_vector_paths_bit_exact(oracle, gpu, shape, offset):
     """Widths that are not a multiple of 4 and inputs that are not 16-byte aligned take the one-wave-
-    per-row kernel; 2052 features take the vector kernel with several groups per lane."""
+    per-row kernel; rows of more than 64 4-feature groups take the long-row kernel; the rest take the
+    register kernel (power-of-two lanes per row, idle lanes when F/4 is not a power of two, row
+    counts that leave a partial last block)."""
     import torch
     from tcc_spmm_amd.device import quantize_features_int8
     s, f = shape
