@@ -2,7 +2,8 @@
 
 HIP sources (*.hip) go through hipcc for gfx950 with packed-FP32 instructions disabled; host-only
 C++ sources (*.cpp) go through g++ against the ROCm headers. Objects land in tcc_spmm_amd/_build/,
-the library in tcc_spmm_amd/libtcc_spmm.so. Run ``python -m tcc_spmm_amd.build``.
+the library in tcc_spmm_amd/libtcc_spmm.so. The command-line harness (cli/tcc_spmm_run.cpp) is linked
+against it as tcc_spmm_amd/tcc_spmm_run. Run ``python -m tcc_spmm_amd.build``.
 """
 from __future__ import annotations
 
@@ -18,6 +19,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtcc_spmm.so"
+CLI_SRC = PKG / "cli" / "tcc_spmm_run.cpp"
+CLI = PKG / "tcc_spmm_run"
 ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("TCC_OFFLOAD_ARCH", "gfx950")
 
@@ -62,9 +65,22 @@ def build(verbose: bool = False) -> pathlib.Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {shlex.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_cli()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {CLI}")
     return LIB
+
+
+def build_cli() -> pathlib.Path:
+    """Link the command-line harness against the in-tree library (found at run time via $ORIGIN)."""
+    tmp = CLI.with_suffix(".tmp")
+    cmd = [os.environ.get("CXX", "g++"), *CXX_FLAGS, "-o", str(tmp), str(CLI_SRC), f"-L{PKG}", "-ltcc_spmm",
+           "-Wl,-rpath,$ORIGIN", f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"CLI build failed: {shlex.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, CLI)
+    return CLI
 
 
 def build_oracle(verbose: bool = False) -> None:

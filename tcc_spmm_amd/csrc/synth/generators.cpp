@@ -17,6 +17,8 @@
 //   t<rows>_<deg>_<seed>  square test matrix with `deg` distinct uniform columns per row.
 // Columns of a row are drawn without replacement; every generated CSR is then passed through
 // makeCanonicalCsr.
+#include "generators.h"
+
 #include "../parallel.h"
 #include "format/csr.h"
 #include "tcc_spmm_c.h"
@@ -305,6 +307,50 @@ Csr makeC5() {
 
 } // namespace
 
+SyntheticCsr makeSyntheticCsr(const std::string& name) {
+    Csr a;
+    if (name == "c1")
+        a = makeUniform(4096, 16, 0);
+    else if (name == "c2")
+        a = makeC2();
+    else if (name == "c3" || name == "c4")
+        a = makeC3();
+    else if (name == "c5")
+        a = makeC5();
+    else if (name.size() > 1 && name[0] == 't') {
+        unsigned long n = 0, deg = 0, seed = 0;
+        if (std::sscanf(name.c_str() + 1, "%lu_%lu_%lu", &n, &deg, &seed) != 3 || !n)
+            throw std::invalid_argument("test config is t<rows>_<deg>_<seed>");
+        a = makeUniform(std::uint32_t(n), std::uint32_t(deg), seed);
+    } else {
+        throw std::invalid_argument("unknown synthetic config: " + name);
+    }
+    CsrMatrix csr = makeCanonicalCsr(a.rows, a.cols, std::uint32_t(a.columns.size()),
+                                     a.offsets.data(), a.columns.data(), a.values.data());
+    return {a.rows, a.cols, std::move(csr)};
+}
+
+void makeSyntheticFeatures(std::uint32_t sources, std::uint32_t features, std::uint64_t seed,
+                           float stddev, float outlierFraction, float outlierScale, float* out) {
+    tcc::parallelChunks(sources, std::min<std::size_t>(sources, 4096),
+                        [&](std::size_t, std::size_t r0, std::size_t r1) {
+                            for (std::size_t r = r0; r < r1; ++r) {
+                                Rng g(seed, r);
+                                const bool outlier = g.uniform() < outlierFraction;
+                                const double mul = stddev * (outlier ? outlierScale : 1.0f);
+                                float* row = out + r * features;
+                                for (std::uint32_t f = 0; f < features; f += 2) {
+                                    // Box-Muller on (0,1] x [0,1)
+                                    const double u1 = 1.0 - g.uniform(), u2 = g.uniform();
+                                    const double rad = std::sqrt(-2.0 * std::log(u1));
+                                    row[f] = float(mul * rad * std::cos(6.283185307179586 * u2));
+                                    if (f + 1 < features)
+                                        row[f + 1] = float(mul * rad * std::sin(6.283185307179586 * u2));
+                                }
+                            }
+                        });
+}
+
 // Implemented in capi.cpp: wraps a CsrMatrix into the opaque handle.
 extern "C" int tccWrapCsr(CsrMatrix&& csr, tcc_csr** out);
 extern "C" void tccSetLastError(const char* message);
@@ -312,29 +358,10 @@ extern "C" void tccSetLastError(const char* message);
 extern "C" int tcc_synth_csr(const char* config, std::uint32_t* rows, std::uint32_t* cols,
                              tcc_csr** out) {
     try {
-        const std::string name = config ? config : "";
-        Csr a;
-        if (name == "c1")
-            a = makeUniform(4096, 16, 0);
-        else if (name == "c2")
-            a = makeC2();
-        else if (name == "c3" || name == "c4")
-            a = makeC3();
-        else if (name == "c5")
-            a = makeC5();
-        else if (name.size() > 1 && name[0] == 't') {
-            unsigned long n = 0, deg = 0, seed = 0;
-            if (std::sscanf(name.c_str() + 1, "%lu_%lu_%lu", &n, &deg, &seed) != 3 || !n)
-                throw std::invalid_argument("test config is t<rows>_<deg>_<seed>");
-            a = makeUniform(std::uint32_t(n), std::uint32_t(deg), seed);
-        } else {
-            throw std::invalid_argument("unknown synthetic config: " + name);
-        }
-        CsrMatrix csr = makeCanonicalCsr(a.rows, a.cols, std::uint32_t(a.columns.size()),
-                                         a.offsets.data(), a.columns.data(), a.values.data());
+        SyntheticCsr a = makeSyntheticCsr(config ? config : "");
         *rows = a.rows;
         *cols = a.cols;
-        return tccWrapCsr(std::move(csr), out);
+        return tccWrapCsr(std::move(a.csr), out);
     } catch (const std::invalid_argument& e) {
         tccSetLastError(e.what());
         return TCC_INVALID_ARGUMENT;
@@ -351,24 +378,7 @@ extern "C" int tcc_synth_features(std::uint32_t sources, std::uint32_t features,
                                   float stddev, float outlierFraction, float outlierScale,
                                   float* out) {
     try {
-        tcc::parallelChunks(sources, std::min<std::size_t>(sources, 4096),
-                            [&](std::size_t, std::size_t r0, std::size_t r1) {
-                                for (std::size_t r = r0; r < r1; ++r) {
-                                    Rng g(seed, r);
-                                    const bool outlier = g.uniform() < outlierFraction;
-                                    const double mul = stddev * (outlier ? outlierScale : 1.0f);
-                                    float* row = out + r * features;
-                                    for (std::uint32_t f = 0; f < features; f += 2) {
-                                        // Box-Muller on (0,1] x [0,1)
-                                        const double u1 = 1.0 - g.uniform(), u2 = g.uniform();
-                                        const double rad = std::sqrt(-2.0 * std::log(u1));
-                                        row[f] = float(mul * rad * std::cos(6.283185307179586 * u2));
-                                        if (f + 1 < features)
-                                            row[f + 1] =
-                                                float(mul * rad * std::sin(6.283185307179586 * u2));
-                                    }
-                                }
-                            });
+        makeSyntheticFeatures(sources, features, seed, stddev, outlierFraction, outlierScale, out);
         return TCC_OK;
     } catch (const std::exception& e) {
         tccSetLastError(e.what());

@@ -20,7 +20,8 @@ def pytest_configure(config):
 
 def _ensure_built():
     lib = ROOT / "tcc_spmm_amd" / "libtcc_spmm.so"
-    if not lib.exists():
+    cli = ROOT / "tcc_spmm_amd" / "tcc_spmm_run"
+    if not lib.exists() or not cli.exists():
         subprocess.run([sys.executable, "-m", "tcc_spmm_amd.build"], cwd=ROOT, check=True)
     orc = ROOT / "oracle" / "_build" / "liboracle.so"
     if not orc.exists():
