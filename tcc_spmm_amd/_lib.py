@@ -90,6 +90,14 @@ def lib() -> C.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise OSError(f"{LIB_PATH} is missing: run `python -m tcc_spmm_amd.build` first")
+        # One HIP runtime per process: PyTorch ships its own libamdhip64, and a library loaded
+        # before it binds the system copy, after which the two runtimes do not share the device
+        # (calls through the library then report "no ROCm-capable device"). Importing torch first
+        # makes the library bind torch's runtime, the one torch tensors and streams belong to.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = C.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

@@ -10,7 +10,8 @@
 //   A (features x slots): the 8 slot rows of the X slice are gathered with one dwordx4 load per
 //   lane (lane L: 16-byte tile L & 7 of slot L >> 3) and stored to LDS as [slot][128 bytes].
 //   Lane l then reads dword l & 31 of slots 4h..4h+3 (h = l >> 5): byte b of that dword is block
-//   b's feature for M index l & 31, so each lane dequantizes 16 bytes (4 slots x 4 blocks).
+//   b's feature for M index l & 31, so each lane dequantizes 16 bytes (4 slots x 4 blocks), with
+//   the four slots' scale mantissas read from LDS as one 16-byte broadcast.
 //   B (slots x rows): an LDS table [32 rows][8 slots] of f16 A values; lane l reads row l & 31,
 //   slots 4h..4h+3. Rows of row groups the panel's bucket does not touch hold 0.
 //   D: lane l holds row l & 31 and, per block, M indices 8i + 4h + j (register 4i + j).
@@ -27,7 +28,8 @@
 // v_mfma_f32_32x32x2_f32 on tf32(a) * 2^kShift and the TF32 features.
 //
 // The panels are walked by a three-stage software pipeline (metadata two panels ahead; scales, A
-// values and X one panel ahead) whose memory operations are identical on every path.
+// values and X one panel ahead) whose memory operations are identical on every path. The kernel
+// runs four waves per SIMD (128 registers each, accumulators included).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes an agent-scope acq_rel
@@ -43,6 +45,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <stdexcept>
+#include <type_traits>
 
 namespace {
 
@@ -57,7 +60,10 @@ constexpr unsigned kSlice = 128;
 constexpr unsigned kNoPartial = 0xFFFFFFFFu;
 constexpr int kShift = 10;
 constexpr float kUnshift = 1.0f / 1024.0f;
-constexpr int kNt = 2; // buffer cache policy: nontemporal (streamed once)
+// Buffer cache policy of the A stream (sourceIds, sourceMetadata, values): the default. The
+// nontemporal hint (2) was measured to raise L2 misses of the gathered X rows by about 1.5 GB per
+// c3 F128 launch.
+constexpr int kNt = 0;
 
 // TF32 rounding from its definition: keep 10 explicit mantissa bits, round to nearest with ties
 // away from zero (adding half an ulp to the sign-magnitude encoding), carry into the exponent.
@@ -213,21 +219,21 @@ __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned 
 // ------------------------------------------------------------------------------------------------
 // Compute
 
-// Slots of dword `d`: bytes 0..3 (blocks 0..3) sign-extended and multiplied by `factor` of slot J,
-// taken from lane J of the lane's 16-lane row (DPP row broadcast). The four conversions ahead of
-// the first DPP read cover the VALU-write -> DPP-read hazard.
-template <unsigned J>
-__device__ __forceinline__ void scaleBytes(unsigned d, float factor, float (&q)[4]) {
-    asm("v_cvt_f32_i32_sdwa %0, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f32_i32_sdwa %2, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-        "v_cvt_f32_i32_sdwa %3, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
-        "v_mul_f32_dpp %0, %5, %0 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %1, %5, %1 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %2, %5, %2 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %3, %5, %3 row_newbcast:%6 row_mask:0xf bank_mask:0xf"
-        : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3])
-        : "v"(d), "v"(factor), "i"(J));
+// Block B of the lane's four slots: byte B of d0..d3 (slots 4h + 0..3) sign-extended to FP32 by
+// SDWA conversions, then multiplied by the slots' scale mantissas (plain multiplies: a DPP operand
+// would cost about twice the issue time of each multiply).
+template <unsigned B>
+__device__ __forceinline__ void scaleBlock(unsigned d0, unsigned d1, unsigned d2, unsigned d3,
+                                           const f32x4& mant, float (&q)[4]) {
+    float c[4];
+    asm("v_cvt_f32_i32_sdwa %0, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%5) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%6) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%7) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8"
+        : "=v"(c[0]), "=v"(c[1]), "=v"(c[2]), "=v"(c[3])
+        : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "i"(B));
+#pragma unroll
+    for (unsigned i = 0; i < 4; ++i) q[i] = c[i] * mant[i];
 }
 
 // TF32-round two values and pack them as f16 (round toward zero after adding half an ulp).
@@ -240,6 +246,7 @@ struct Lds {
     _Float16* table16; // [32 rows][8 slots] a' (f16 path)
     float* table32;    // [32 rows][8 slots] tf32(a) * 2^kShift (FP32 path)
     u32x4* xtile;      // [8 slots][128 bytes] X slice rows of the panel
+    float* mant;       // [8 slots] scale mantissas of the panel
     unsigned char* redo; // [384 + 64]: byte i = 1 when panel begin + i needs the FP32 path (a task
                          // has <= 384 panels); bytes 384.. absorb the other lanes' stores
 };
@@ -278,28 +285,28 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
         lds.table16[64 * (G < 4 ? G : j) + lane] = static_cast<_Float16>(useF16 ? ap[j] : 0.0f);
     lds.xtile[lane] = s.x;
     const unsigned m = lane & 31, h = lane >> 5;
-    // Lanes 16q + j (j < 4) need the mantissa of slot j + 4 (q >> 1) for the DPP broadcast; lane
-    // k < 8 holds slot k.
-    const float mant = __builtin_amdgcn_frexp_mantf(s.scale);
-    const float mantB = __int_as_float(
-        __builtin_amdgcn_ds_bpermute(int(((lane & 3) + 4 * h) * 4), __float_as_int(mant)));
+    // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3.
+    lds.mant[lane & 7] = __builtin_amdgcn_frexp_mantf(s.scale);
     __syncthreads();
+    const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
     const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
     const unsigned d0 = xw[(4 * h + 0) * 32], d1 = xw[(4 * h + 1) * 32];
     const unsigned d2 = xw[(4 * h + 2) * 32], d3 = xw[(4 * h + 3) * 32];
     const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
-    float q0[4], q1[4], q2[4], q3[4];
-    scaleBytes<0>(d0, mantB, q0);
-    scaleBytes<1>(d1, mantB, q1);
-    scaleBytes<2>(d2, mantB, q2);
-    scaleBytes<3>(d3, mantB, q3);
-#pragma unroll
-    for (unsigned blk = 0; blk < 4; ++blk) {
-        const f16x2 lo = roundPack(q0[blk], q1[blk]);
-        const f16x2 hi = roundPack(q2[blk], q3[blk]);
-        const f16x4 av = __builtin_bit_cast(f16x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3));
-        acc[blk] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[blk], 0, 0, 0);
-    }
+    // One block at a time (four live temporaries instead of sixteen keeps the kernel within the
+    // 128 registers of four waves per SIMD).
+    auto block = [&](auto blk) {
+        constexpr unsigned B = decltype(blk)::value;
+        float q[4];
+        scaleBlock<B>(d0, d1, d2, d3, mant, q);
+        const f16x4 av = __builtin_bit_cast(
+            f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
+        acc[B] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[B], 0, 0, 0);
+    };
+    block(std::integral_constant<unsigned, 0>{});
+    block(std::integral_constant<unsigned, 1>{});
+    block(std::integral_constant<unsigned, 2>{});
+    block(std::integral_constant<unsigned, 3>{});
     __syncthreads();
     return useF16;
 }
@@ -495,11 +502,14 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
     return xcd * q + min(xcd, r) + j;
 }
 
+// Four waves per SIMD: the accumulators live in ordinary VGPRs and the kernel fits 128 registers.
 template <unsigned Features, bool Wide>
-__global__ __launch_bounds__(kWave) void spmmInt8Kernel(KernelArgs a) {
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) void spmmInt8Kernel(
+    KernelArgs a) {
     __shared__ __align__(16) _Float16 table16[256];
     __shared__ __align__(16) float table32[256];
     __shared__ __align__(16) u32x4 xtile[64];
+    __shared__ __align__(16) float mant[8];
     __shared__ unsigned char redo[384 + 64];
     __shared__ unsigned lastFlag;
     const unsigned lane = threadIdx.x;
@@ -507,7 +517,7 @@ __global__ __launch_bounds__(kWave) void spmmInt8Kernel(KernelArgs a) {
     const Sw32Task task = a.m.tasks[xcdTask(blockIdx.x, a.m.taskCount)];
     const unsigned sw = task.sw;
     const Loader<Wide> ld(a, task.begin, task.end, Features, slice);
-    const Lds lds{table16, table32, xtile, redo};
+    const Lds lds{table16, table32, xtile, mant, redo};
 
     f32x16 acc[4];
 #pragma unroll
