@@ -242,13 +242,21 @@ __device__ __forceinline__ f16x2 roundPack(float a, float b) {
                                       __uint_as_float(__float_as_uint(b) + 0x1000u));
 }
 
+// LDS handoff between the lanes of the workgroup's single wave: the wave's LDS operations execute
+// in order, so only the compiler has to be kept from moving memory accesses across this point.
+__device__ __forceinline__ void waveSync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 struct Lds {
     _Float16* table16; // [32 rows][8 slots] a' (f16 path)
     float* table32;    // [32 rows][8 slots] tf32(a) * 2^kShift (FP32 path)
     u32x4* xtile;      // [8 slots][128 bytes] X slice rows of the panel
     float* mant;       // [8 slots] scale mantissas of the panel
-    unsigned char* redo; // [384 + 64]: byte i = 1 when panel begin + i needs the FP32 path (a task
-                         // has <= 384 panels); bytes 384.. absorb the other lanes' stores
+    unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
+                          // the FP32 path, in the order found (a task has <= 384 panels)
 };
 
 // Entry j of a stage as tf32(a) (0 when absent).
@@ -274,8 +282,8 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
         const float at = stageTf32<Wide>(s, j);
         ap[j] = __builtin_amdgcn_ldexpf(at, e + kShift);
         // f16 normal range [2^-14, 2^16): biased FP32 exponent 113..142.
-        exact = exact && (at == 0.0f ||
-                          (((__float_as_uint(ap[j]) >> 23) & 0xFFu) - 113u <= 29u && scaleNormal));
+        exact = exact & ((at == 0.0f) |
+                         ((((__float_as_uint(ap[j]) >> 23) & 0xFFu) - 113u <= 29u) & scaleNormal));
     }
     // A panel without exact f16 operands still runs its MFMAs (straight-line accumulators), on an
     // all-zero table; the FP32 pass adds it later.
@@ -287,7 +295,7 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
     const unsigned m = lane & 31, h = lane >> 5;
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3.
     lds.mant[lane & 7] = __builtin_amdgcn_frexp_mantf(s.scale);
-    __syncthreads();
+    waveSync();
     const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
     const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
     const unsigned d0 = xw[(4 * h + 0) * 32], d1 = xw[(4 * h + 1) * 32];
@@ -307,7 +315,7 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
     block(std::integral_constant<unsigned, 1>{});
     block(std::integral_constant<unsigned, 2>{});
     block(std::integral_constant<unsigned, 3>{});
-    __syncthreads();
+    waveSync();
     return useF16;
 }
 
@@ -321,7 +329,7 @@ __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups,
         lds.table32[64 * g + lane] =
             ((groups >> g) & 1u) ? __builtin_amdgcn_ldexpf(stageTf32<Wide>(s, g), kShift) : 0.0f;
     lds.xtile[lane] = s.x;
-    __syncthreads();
+    waveSync();
     const unsigned m = lane & 31, h = lane >> 5;
     const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
 #pragma unroll
@@ -337,7 +345,7 @@ __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups,
             acc[blk] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, b, acc[blk], 0, 0, 0);
         }
     }
-    __syncthreads();
+    waveSync();
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -371,20 +379,23 @@ struct TaskWalk {
     unsigned begin, end;     // the task's panels
     unsigned lane;
     Lds lds;
+    unsigned redoCount;      // entries in lds.redo
 };
 
-// Flags panel `panel` (wave-uniform `redo`) for the FP32 pass: lane 0 writes the panel's flag byte,
-// the other lanes a byte of their own, so the store is neither divergent nor conflicting.
-__device__ __forceinline__ void flagRedo(const TaskWalk& w, unsigned panel, bool redo) {
-    const unsigned i = panel - w.begin;
-    unsigned char* dst = w.lane == 0 ? w.lds.redo + i : w.lds.redo + 384 + w.lane;
-    *dst = redo ? 1 : 0;
+// Queues panel `panel` for the FP32 pass when `redo` (wave-uniform) is set. The branch is taken only
+// for panels whose operands do not fit f16, so the common path costs one scalar branch; the queue
+// length lives in a scalar register.
+__device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo) {
+    if (__builtin_expect(redo, 0)) { // wave-uniform and rare
+        if (w.lane == 0) w.lds.redo[w.redoCount] = static_cast<unsigned short>(panel - w.begin);
+        ++w.redoCount;
+    }
 }
 
 // The panels [lo, hi) of kind G, three-stage pipelined, two panels per iteration with the odd one
 // after the loop (a single exit keeps the accumulators in place).
 template <unsigned G, class Ld>
-__device__ __forceinline__ void walkPanels(const Ld& ld, const TaskWalk& w, unsigned lo,
+__device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4]) {
     if (lo >= hi) return;
     const unsigned n = hi - lo, lane = w.lane;
@@ -441,7 +452,7 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
                                          unsigned end, unsigned lane, const Lds& lds,
                                          f32x16 (&acc)[4]) {
     if (begin >= end) return;
-    const TaskWalk w{offsets, begin, end, lane, lds};
+    TaskWalk w{offsets, begin, end, lane, lds, 0u};
     auto clipLo = [&](unsigned t) { return max(offsets[t], begin); };
     auto clipHi = [&](unsigned t) { return min(offsets[t], end); };
     walkPanels<0>(ld, w, clipLo(1), clipHi(2), acc);
@@ -450,21 +461,14 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
     walkPanels<3>(ld, w, clipLo(4), clipHi(5), acc);
     walkPanels<kShared>(ld, w, clipLo(5), clipHi(16), acc);
     // Panels whose scaled A values leave f16's normal range, again with exact FP32 operands.
-    __syncthreads();
-    const unsigned n = end - begin;
+    waveSync();
 #pragma unroll 1
-    for (unsigned base = 0; base < n; base += 64) {
-        const bool flagged = base + lane < n && lds.redo[base + lane] != 0;
-        std::uint64_t bits = __builtin_amdgcn_ballot_w64(flagged);
-#pragma unroll 1
-        while (bits) {
-            const unsigned panel = begin + base + unsigned(__builtin_ctzll(bits));
-            bits &= bits - 1;
-            const unsigned groups = groupsOf(offsets, panel);
-            Stage st;
-            loadStage<kShared>(ld, ld.meta8(panel, lane), groups, lane, st);
-            computePanelF32<Ld::kWide>(st, groups, lane, lds, acc);
-        }
+    for (unsigned i = 0; i < w.redoCount; ++i) {
+        const unsigned panel = begin + __builtin_amdgcn_readfirstlane(lds.redo[i]);
+        const unsigned groups = groupsOf(offsets, panel);
+        Stage st;
+        loadStage<kShared>(ld, ld.meta8(panel, lane), groups, lane, st);
+        computePanelF32<Ld::kWide>(st, groups, lane, lds, acc);
     }
 }
 
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     __shared__ __align__(16) float table32[256];
     __shared__ __align__(16) u32x4 xtile[64];
     __shared__ __align__(16) float mant[8];
-    __shared__ unsigned char redo[384 + 64];
+    __shared__ unsigned short redo[384];
     __shared__ unsigned lastFlag;
     const unsigned lane = threadIdx.x;
     const unsigned slice = blockIdx.y;
@@ -543,14 +547,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     // Completion ticket: the acq_rel RMW at agent scope publishes this task's partial tiles and,
     // for the last arriver, makes every other task's tiles visible (the XCD L2s are not coherent
     // with each other, so the release writes back and the acquire invalidates).
-    __syncthreads();
+    waveSync();
     if (lane == 0) {
         unsigned* counter = a.counters + std::size_t(sw) * (Features / kSlice) + slice;
         const unsigned ticket =
             __builtin_amdgcn_atomic_inc32(counter, task.chunks - 1, __ATOMIC_ACQ_REL, "agent");
         lastFlag = ticket == task.chunks - 1;
     }
-    __syncthreads();
+    waveSync();
     if (!lastFlag) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // Merge the slice: each lane sums columns lane and lane + 64, adding the partial tiles in
