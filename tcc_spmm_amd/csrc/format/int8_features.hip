@@ -119,18 +119,22 @@ __global__ __launch_bounds__(256) void quantizeRowsLong(const f32x4* __restrict_
     for (unsigned j = lane; j < groups; j += kWave) qr[j] = quantizeGroup(xr[j], s);
 }
 
-__global__ __launch_bounds__(256) void packTiles(const uint4* __restrict__ q,
-                                                 uint4* __restrict__ out, std::size_t tiles) {
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// One thread per 16-byte tile; q is read once and packed written once, so both use nontemporal
+// access (measured on c3: 6.5 TB/s against 6.0 with the default policy).
+__global__ __launch_bounds__(256) void packTiles(const u32x4* __restrict__ q,
+                                                 u32x4* __restrict__ out, std::size_t tiles) {
     const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (t >= tiles) return;
-    const uint4 w = q[t];
+    const u32x4 w = __builtin_nontemporal_load(q + t);
     // v_perm_b32 selectors: bytes 0-3 pick from the second operand, 4-7 from the first.
-    uint4 r;
+    u32x4 r;
     r.x = __builtin_amdgcn_perm(w.z, w.x, 0x05010400u); // q0  q8  q1  q9
     r.y = __builtin_amdgcn_perm(w.z, w.x, 0x07030602u); // q2  q10 q3  q11
     r.z = __builtin_amdgcn_perm(w.w, w.y, 0x05010400u); // q4  q12 q5  q13
     r.w = __builtin_amdgcn_perm(w.w, w.y, 0x07030602u); // q6  q14 q7  q15
-    out[t] = r;
+    __builtin_nontemporal_store(r, out + t);
 }
 
 __global__ __launch_bounds__(256) void packPairs(const std::uint8_t* __restrict__ q,
@@ -193,7 +197,7 @@ void packFeaturesInt8x16(const std::int8_t* q, std::int8_t* packed, std::uint32_
         const std::size_t tiles = bytes / 16;
         const std::size_t blocks = (tiles + 255) / 256;
         hipLaunchKernelGGL(packTiles, dim3(unsigned(blocks)), dim3(256), 0, stream,
-                           reinterpret_cast<const uint4*>(q), reinterpret_cast<uint4*>(packed),
+                           reinterpret_cast<const u32x4*>(q), reinterpret_cast<u32x4*>(packed),
                            tiles);
     } else {
         const std::size_t pairs = bytes / 2;
