@@ -13,7 +13,8 @@ Roofline: algorithmic bytes per launch B_alg = B_A + B_X + B_Y + B_P, computed f
   B_P = 64 F K                                                   (partial tiles written + read once)
 achieved = B_alg / kernel time, peak = 8.0e12 B/s. `traffic` (HBM bytes per launch: rocprofv3
 FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a 1 GiB copy) is read from
-profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present.
+profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present;
+`traffic_bw` is that traffic over the measured time (the memory system's actual load).
 
 cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over a bounded prefix of
 SWs (~10 s of CPU work), extrapolated by SW count to one full SpMM.
@@ -208,9 +209,16 @@ def main() -> None:
         prof = ROOT / "profiles" / f"spmmInt8Kernel_{args.config}_f{feats}_counters.json"
         if prof.exists():
             traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
+        # Measured HBM traffic (L2 misses and writes, rocprof counters of this workload) over the
+        # kernel time: how much of the memory system the launch uses, as opposed to `achieved`,
+        # which counts each algorithmic byte once.
+        traffic_bw = None
+        if traffic:
+            tb = traffic / (ms * 1e-3)
+            traffic_bw = {"gbps": round(tb / 1e9, 1), "frac_of_peak": round(tb / HBM_PEAK, 4)}
         results[feats] = {
             "ms": round(ms, 4), "means_ms": [round(m, 4) for m in means], "feature_prep": prep,
-            "gbps": round(achieved / 1e9, 1), "bytes": b, "y00_07": y0,
+            "gbps": round(achieved / 1e9, 1), "bytes": b, "y00_07": y0, "traffic_bw": traffic_bw,
             "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1),
                          "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK, 4), "traffic": traffic},
@@ -235,7 +243,7 @@ def main() -> None:
                    "partial_count": stats["partial_count"], "panels": stats["panels"]},
         "gbps": r["gbps"], "roofline": r["roofline"], "cpu_baseline": base,
         "f256": results.get(256),
-        "f128_detail": {k: r[k] for k in ("means_ms", "bytes", "y00_07", "feature_prep")},
+        "f128_detail": {k: r[k] for k in ("means_ms", "bytes", "y00_07", "feature_prep", "traffic_bw")},
     }
     print(json.dumps(line), flush=True)
 
