@@ -1,10 +1,11 @@
 // Fused INT8-dequantization SpMM for MI355X (gfx950, wave64): Y = A x tf32(dequant(X)).
 //
 // Work decomposition
-//   One wavefront per workgroup (task, slice): task = one Sw32Task (<= 384 panels of one 32-row
-//   SW), slice = 128 features. The wave walks the task's panels once, in order, and accumulates
-//   all 32 rows x 128 features of the SW: four v_mfma_f32_32x32x8_f16 per panel (one per 32-feature
-//   block; M = features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators.
+//   One wavefront per workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW). The wave
+//   walks the task's panels once, in order, and accumulates all 32 rows x F features of the SW:
+//   four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block; M =
+//   features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per slice.
+//   F256 runs both slices in the same wave, so the A side of a panel is loaded and built once.
 //
 // Operands of one panel
 //   A (features x slots): the 8 slot rows of the X slice are gathered with one dwordx4 load per
@@ -28,13 +29,13 @@
 // v_mfma_f32_32x32x2_f32 on tf32(a) * 2^kShift and the TF32 features.
 //
 // The panels are walked by a three-stage software pipeline (metadata two panels ahead; scales, A
-// values and X one panel ahead) whose memory operations are identical on every path. The kernel
-// runs four waves per SIMD (128 registers each, accumulators included).
+// values and X one panel ahead) whose memory operations are identical on every path. F128 runs four
+// waves per SIMD (128 registers each, accumulators included), F256 two (192 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
-// `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes an agent-scope acq_rel
-// wrapping ticket on counters[sw * (F/128) + slice] with limit chunks - 1, so the counter returns
-// to zero by itself; the task whose ticket is chunks - 1 merges all partial tiles of the SW's
+// `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes, per slice, an agent-scope
+// acq_rel wrapping ticket on counters[sw * (F/128) + slice] with limit chunks - 1, so the counter
+// returns to zero by itself; the task whose ticket is chunks - 1 merges all partial tiles of the SW's
 // slice in partialIds order starting from 0.0f and writes Y. No float atomics, no spin-waits.
 #include "spmm.h"
 #include "hip_support.h"
@@ -111,11 +112,9 @@ struct Loader<false> {
     unsigned first;     // task.begin: panel offsets are relative to it
     unsigned vbase;     // value base of the task's first slot, the smallest of the task
     unsigned xShift;    // log2(features)
-    unsigned sliceByte; // slice * 128
 
-    __device__ Loader(const KernelArgs& a, unsigned begin, unsigned end, unsigned features,
-                      unsigned slice)
-        : first(begin), xShift(features == 256 ? 8u : 7u), sliceByte(slice * kSlice) {
+    __device__ Loader(const KernelArgs& a, unsigned begin, unsigned end, unsigned features)
+        : first(begin), xShift(features == 256 ? 8u : 7u) {
         const std::size_t slot0 = std::size_t(begin) * 8;
         // Value bases grow in slot order (reference src/format/sw32.cpp:131-138) and every panel
         // starts with a real slot, so the first slot of the task has the smallest base.
@@ -145,9 +144,10 @@ struct Loader<false> {
         const unsigned off = present ? (idx - vbase) * 4u : 0xFFFFFFFCu;
         return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vals, off, 0, kNt));
     }
-    __device__ u32x4 tile(unsigned src, unsigned lane) const {
-        return __builtin_amdgcn_raw_buffer_load_b128(x, (src << xShift) + 16 * (lane & 7),
-                                                     int(sliceByte), 0);
+    // 16-byte tile `lane & 7` of slice k of the packed X row of `src`.
+    __device__ u32x4 tile(unsigned src, unsigned lane, unsigned k) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(x, (src << xShift) + 16 * (lane & 7) + kSlice * k,
+                                                     0, 0);
     }
 };
 
@@ -155,11 +155,10 @@ template <>
 struct Loader<true> {
     static constexpr bool kWide = true;
     const KernelArgs* a;
-    const std::int8_t* xSlice;
     unsigned features;
 
-    __device__ Loader(const KernelArgs& args, unsigned, unsigned, unsigned f, unsigned slice)
-        : a(&args), xSlice(args.packedX + slice * kSlice), features(f) {}
+    __device__ Loader(const KernelArgs& args, unsigned, unsigned, unsigned f)
+        : a(&args), features(f) {}
     __device__ Meta meta8(unsigned panel, unsigned lane) const {
         const std::size_t first = std::size_t(panel) * 8;
         const std::uint64_t md =
@@ -173,9 +172,9 @@ struct Loader<true> {
     __device__ float value(unsigned idx, bool) const {
         return __builtin_nontemporal_load(a->m.values + idx);
     }
-    __device__ u32x4 tile(unsigned src, unsigned lane) const {
-        return *reinterpret_cast<const u32x4*>(
-            xSlice + std::size_t(min(src, a->cols - 1)) * features + 16 * (lane & 7));
+    __device__ u32x4 tile(unsigned src, unsigned lane, unsigned k) const {
+        return *reinterpret_cast<const u32x4*>(a->packedX + std::size_t(min(src, a->cols - 1)) * features +
+                                               16 * (lane & 7) + kSlice * k);
     }
 };
 
@@ -187,11 +186,11 @@ struct Stage {     // one panel, ready to compute
     float scale;   // lane L: scale of slot L & 7
     float v[4];    // lane L: raw A value of (slot L & 7, row 8g + (L >> 3)); v[0] for kind G < 4
     unsigned bits; // bit g: that entry is present (wide loader only; narrow reads 0 instead)
-    u32x4 x;       // 16-byte tile L & 7 of the X row of slot L >> 3
+    u32x4 x[2];    // 16-byte tile L & 7 of the X row of slot L >> 3, per slice of the wave
 };
 
 // Stage 2 of one panel of kind G (row groups `groups` when G == kShared).
-template <unsigned G, class Ld>
+template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned groups,
                                           unsigned lane, Stage& s) {
     // Padding slots (source UINT32_MAX, metadata 0) have an empty row mask; their scale and X tile
@@ -213,7 +212,8 @@ __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned 
             s.v[j] = ld.value(idx, present);
         }
     }
-    s.x = ld.tile(m.gather, lane);
+#pragma unroll
+    for (unsigned k = 0; k < S; ++k) s.x[k] = ld.tile(m.gather, lane, k);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -269,9 +269,9 @@ __device__ __forceinline__ float stageTf32(const Stage& s, unsigned j) {
 // is (8g + (lane >> 3)) * 8 + k = 64g + lane. Kind G < 4 writes only row group G (the others hold
 // 0 for the whole bucket). Returns whether every entry of the panel has an exact f16 a'
 // (wave-uniform); if not, the panel contributes nothing here.
-template <bool Wide, unsigned G>
+template <bool Wide, unsigned G, unsigned S>
 __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups, unsigned lane,
-                                                const Lds& lds, f32x16 (&acc)[4]) {
+                                                const Lds& lds, f32x16 (&acc)[4 * S]) {
     const int e = __builtin_amdgcn_frexp_expf(s.scale);
     const bool scaleNormal = e > -126;
     bool exact = true;
@@ -291,58 +291,63 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
 #pragma unroll
     for (unsigned j = 0; j < kCount; ++j)
         lds.table16[64 * (G < 4 ? G : j) + lane] = static_cast<_Float16>(useF16 ? ap[j] : 0.0f);
-    lds.xtile[lane] = s.x;
+#pragma unroll
+    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
     const unsigned m = lane & 31, h = lane >> 5;
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3.
     lds.mant[lane & 7] = __builtin_amdgcn_frexp_mantf(s.scale);
     waveSync();
     const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
-    const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
-    const unsigned d0 = xw[(4 * h + 0) * 32], d1 = xw[(4 * h + 1) * 32];
-    const unsigned d2 = xw[(4 * h + 2) * 32], d3 = xw[(4 * h + 3) * 32];
     const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
-    // One block at a time (four live temporaries instead of sixteen keeps the kernel within the
-    // 128 registers of four waves per SIMD).
-    auto block = [&](auto blk) {
-        constexpr unsigned B = decltype(blk)::value;
-        float q[4];
-        scaleBlock<B>(d0, d1, d2, d3, mant, q);
-        const f16x4 av = __builtin_bit_cast(
-            f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
-        acc[B] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[B], 0, 0, 0);
-    };
-    block(std::integral_constant<unsigned, 0>{});
-    block(std::integral_constant<unsigned, 1>{});
-    block(std::integral_constant<unsigned, 2>{});
-    block(std::integral_constant<unsigned, 3>{});
+#pragma unroll
+    for (unsigned k = 0; k < S; ++k) {
+        const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile + 64 * k) + m;
+        const unsigned d0 = xw[(4 * h + 0) * 32], d1 = xw[(4 * h + 1) * 32];
+        const unsigned d2 = xw[(4 * h + 2) * 32], d3 = xw[(4 * h + 3) * 32];
+        auto block = [&](auto blk) {
+            constexpr unsigned B = decltype(blk)::value;
+            float q[4];
+            scaleBlock<B>(d0, d1, d2, d3, mant, q);
+            const f16x4 av = __builtin_bit_cast(
+                f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
+            acc[4 * k + B] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + B], 0, 0, 0);
+        };
+        block(std::integral_constant<unsigned, 0>{});
+        block(std::integral_constant<unsigned, 1>{});
+        block(std::integral_constant<unsigned, 2>{});
+        block(std::integral_constant<unsigned, 3>{});
+    }
     waveSync();
     return useF16;
 }
 
 // A shared-kind panel with exact FP32 operands (v_mfma_f32_32x32x2_f32): K = 2 steps over slot
 // pairs (2j, 2j + 1), lane half h taking slot 2j + h, whose scale comes from lane 2j + h.
-template <bool Wide>
+template <bool Wide, unsigned S>
 __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups, unsigned lane,
-                                                const Lds& lds, f32x16 (&acc)[4]) {
+                                                const Lds& lds, f32x16 (&acc)[4 * S]) {
 #pragma unroll
     for (unsigned g = 0; g < 4; ++g)
         lds.table32[64 * g + lane] =
             ((groups >> g) & 1u) ? __builtin_amdgcn_ldexpf(stageTf32<Wide>(s, g), kShift) : 0.0f;
-    lds.xtile[lane] = s.x;
+#pragma unroll
+    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
     waveSync();
     const unsigned m = lane & 31, h = lane >> 5;
-    const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
 #pragma unroll
     for (unsigned j = 0; j < 4; ++j) {
         const unsigned slot = 2 * j + h;
         const float sc =
             __int_as_float(__builtin_amdgcn_ds_bpermute(int(slot * 4), __float_as_int(s.scale)));
-        const unsigned d = xw[slot * 32];
         const float b = lds.table32[m * 8 + slot];
 #pragma unroll
-        for (unsigned blk = 0; blk < 4; ++blk) {
-            const float x = roundTf32(float(int(d << (24 - 8 * blk)) >> 24) * sc);
-            acc[blk] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, b, acc[blk], 0, 0, 0);
+        for (unsigned k = 0; k < S; ++k) {
+            const unsigned d = (reinterpret_cast<const unsigned*>(lds.xtile + 64 * k) + m)[slot * 32];
+#pragma unroll
+            for (unsigned blk = 0; blk < 4; ++blk) {
+                const float x = roundTf32(float(int(d << (24 - 8 * blk)) >> 24) * sc);
+                acc[4 * k + blk] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, b, acc[4 * k + blk], 0, 0, 0);
+            }
         }
     }
     waveSync();
@@ -394,9 +399,9 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 
 // The panels [lo, hi) of kind G, three-stage pipelined, two panels per iteration with the odd one
 // after the loop (a single exit keeps the accumulators in place).
-template <unsigned G, class Ld>
+template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
-                                           unsigned hi, f32x16 (&acc)[4]) {
+                                           unsigned hi, f32x16 (&acc)[4 * S]) {
     if (lo >= hi) return;
     const unsigned n = hi - lo, lane = w.lane;
     if constexpr (G < 4) {
@@ -412,7 +417,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
     const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
     Stage sa, sb;
     unsigned ga = groupsAt(lo);
-    loadStage<G>(ld, ld.meta8(lo, lane), ga, lane, sa);
+    loadStage<G, S>(ld, ld.meta8(lo, lane), ga, lane, sa);
     unsigned g1 = groupsAt(p1), g2 = groupsAt(p2), gb = 0;
     // The loop expects m1's loads to be older than m2's (waits are counted in issue order).
     Meta m1 = ld.meta8(p1, lane);
@@ -424,7 +429,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
     for (unsigned k = 0; k < pairs; ++k) {
         // Panels lo + 2k (in sa) and lo + 2k + 1; stage 2 one panel ahead, stage 1 two.
         gb = g1;
-        loadStage<G>(ld, m1, gb, lane, sb);
+        loadStage<G, S>(ld, m1, gb, lane, sb);
         p = min(p + 1, last);
         m1 = m2;
         g1 = g2;
@@ -433,33 +438,33 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
         // Issue this half's loads before any use of the previous half's: the vmcnt counter is in
         // order, so computing first would wait for loads issued only half an iteration ago.
         __builtin_amdgcn_sched_barrier(0);
-        flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G>(sa, ga, lane, w.lds, acc));
+        flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
         ga = g1;
-        loadStage<G>(ld, m1, ga, lane, sa);
+        loadStage<G, S>(ld, m1, ga, lane, sa);
         p = min(p + 1, last);
         m1 = m2;
         g1 = g2;
         g2 = groupsAt(p);
         m2 = ld.meta8(p, lane);
         __builtin_amdgcn_sched_barrier(0);
-        flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G>(sb, gb, lane, w.lds, acc));
+        flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
     }
-    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G>(sa, ga, lane, w.lds, acc));
+    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
 }
 
-template <class Ld>
+template <unsigned S, class Ld>
 __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, unsigned begin,
                                          unsigned end, unsigned lane, const Lds& lds,
-                                         f32x16 (&acc)[4]) {
+                                         f32x16 (&acc)[4 * S]) {
     if (begin >= end) return;
     TaskWalk w{offsets, begin, end, lane, lds, 0u};
     auto clipLo = [&](unsigned t) { return max(offsets[t], begin); };
     auto clipHi = [&](unsigned t) { return min(offsets[t], end); };
-    walkPanels<0>(ld, w, clipLo(1), clipHi(2), acc);
-    walkPanels<1>(ld, w, clipLo(2), clipHi(3), acc);
-    walkPanels<2>(ld, w, clipLo(3), clipHi(4), acc);
-    walkPanels<3>(ld, w, clipLo(4), clipHi(5), acc);
-    walkPanels<kShared>(ld, w, clipLo(5), clipHi(16), acc);
+    walkPanels<0, S>(ld, w, clipLo(1), clipHi(2), acc);
+    walkPanels<1, S>(ld, w, clipLo(2), clipHi(3), acc);
+    walkPanels<2, S>(ld, w, clipLo(3), clipHi(4), acc);
+    walkPanels<3, S>(ld, w, clipLo(4), clipHi(5), acc);
+    walkPanels<kShared, S>(ld, w, clipLo(5), clipHi(16), acc);
     // Panels whose scaled A values leave f16's normal range, again with exact FP32 operands.
     waveSync();
 #pragma unroll 1
@@ -467,8 +472,8 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
         const unsigned panel = begin + __builtin_amdgcn_readfirstlane(lds.redo[i]);
         const unsigned groups = groupsOf(offsets, panel);
         Stage st;
-        loadStage<kShared>(ld, ld.meta8(panel, lane), groups, lane, st);
-        computePanelF32<Ld::kWide>(st, groups, lane, lds, acc);
+        loadStage<kShared, S>(ld, ld.meta8(panel, lane), groups, lane, st);
+        computePanelF32<Ld::kWide, S>(st, groups, lane, lds, acc);
     }
 }
 
@@ -506,95 +511,133 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
     return xcd * q + min(xcd, r) + j;
 }
 
-// Four waves per SIMD: the accumulators live in ordinary VGPRs and the kernel fits 128 registers.
+// One task over all S = Features / 128 slices of its SW (one wave).
 template <unsigned Features, bool Wide>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) void spmmInt8Kernel(
-    KernelArgs a) {
+__device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex) {
+    constexpr unsigned S = Features / kSlice;
     __shared__ __align__(16) _Float16 table16[256];
     __shared__ __align__(16) float table32[256];
-    __shared__ __align__(16) u32x4 xtile[64];
+    __shared__ __align__(16) u32x4 xtile[64 * S];
     __shared__ __align__(16) float mant[8];
     __shared__ unsigned short redo[384];
-    __shared__ unsigned lastFlag;
+    __shared__ unsigned lastFlag[S];
     const unsigned lane = threadIdx.x;
-    const unsigned slice = blockIdx.y;
-    const Sw32Task task = a.m.tasks[xcdTask(blockIdx.x, a.m.taskCount)];
+    const Sw32Task task = a.m.tasks[taskIndex];
     const unsigned sw = task.sw;
-    const Loader<Wide> ld(a, task.begin, task.end, Features, slice);
+    const Loader<Wide> ld(a, task.begin, task.end, Features);
     const Lds lds{table16, table32, xtile, mant, redo};
 
-    f32x16 acc[4];
+    f32x16 acc[4 * S];
 #pragma unroll
-    for (unsigned b = 0; b < 4; ++b) acc[b] = f32x16{};
-    walkTask(ld, a.m.bucketOffsets + std::size_t(sw) * 17, task.begin, task.end, lane, lds, acc);
+    for (unsigned b = 0; b < 4 * S; ++b) acc[b] = f32x16{};
+    walkTask<S>(ld, a.m.bucketOffsets + std::size_t(sw) * 17, task.begin, task.end, lane, lds, acc);
 #pragma unroll
-    for (unsigned b = 0; b < 4; ++b) acc[b] *= kUnshift; // exact power-of-two scaling back to Y
+    for (unsigned b = 0; b < 4 * S; ++b) acc[b] *= kUnshift; // exact power-of-two scaling back to Y
 
     const unsigned row = lane & 31, h = lane >> 5;
-    const unsigned colBase = slice * kSlice;
+    auto sub = [&](unsigned k) -> const f32x16(&)[4] {
+        return *reinterpret_cast<const f32x16(*)[4]>(&acc[4 * k]);
+    };
     if (task.partial == kNoPartial) {
         const unsigned r = sw * 32 + row;
-        if (r < a.rows)
-            storeRow(acc, a.y + std::size_t(r) * Features + colBase, h, true);
+        if (r < a.rows) {
+#pragma unroll
+            for (unsigned k = 0; k < S; ++k)
+                storeRow(sub(k), a.y + std::size_t(r) * Features + k * kSlice, h, true);
+        }
         return;
     }
     const unsigned rw = row >> 3;
     if ((task.mask >> rw) & 1u) {
         const std::size_t tile = task.partial + __popc(task.mask & ((1u << rw) - 1u));
-        storeRow(acc, a.partials + (tile * 8 + (row & 7)) * Features + colBase, h, false);
+#pragma unroll
+        for (unsigned k = 0; k < S; ++k)
+            storeRow(sub(k), a.partials + (tile * 8 + (row & 7)) * Features + k * kSlice, h,
+                     false);
     }
 
-    // Completion ticket: the acq_rel RMW at agent scope publishes this task's partial tiles and,
-    // for the last arriver, makes every other task's tiles visible (the XCD L2s are not coherent
-    // with each other, so the release writes back and the acquire invalidates).
+    // Completion tickets, one per slice: the acq_rel RMW at agent scope publishes this task's
+    // partial tiles and, for the last arriver, makes every other task's tiles visible (the XCD L2s
+    // are not coherent with each other, so the release writes back and the acquire invalidates).
     waveSync();
     if (lane == 0) {
-        unsigned* counter = a.counters + std::size_t(sw) * (Features / kSlice) + slice;
-        const unsigned ticket =
-            __builtin_amdgcn_atomic_inc32(counter, task.chunks - 1, __ATOMIC_ACQ_REL, "agent");
-        lastFlag = ticket == task.chunks - 1;
+#pragma unroll
+        for (unsigned k = 0; k < S; ++k) {
+            unsigned* counter = a.counters + std::size_t(sw) * S + k;
+            const unsigned ticket =
+                __builtin_amdgcn_atomic_inc32(counter, task.chunks - 1, __ATOMIC_ACQ_REL, "agent");
+            lastFlag[k] = ticket == task.chunks - 1;
+        }
     }
     waveSync();
-    if (!lastFlag) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // Merge the slice: each lane sums columns lane and lane + 64, adding the partial tiles in
-    // partialIds (task) order starting from 0.0f.
-    const unsigned mcol = colBase + lane;
 #pragma unroll 1
-    for (unsigned g = 0; g < 4; ++g) {
-        const Sw32ReduceRange red = a.m.reductions[task.reduceFirst + g];
-        const unsigned row0 = sw * 32 + g * 8;
-        if (row0 >= a.rows) continue;
-        const unsigned valid = min(8u, a.rows - row0);
+    for (unsigned k = 0; k < S; ++k) {
+        if (!lastFlag[k]) continue;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // Merge the slice: each lane sums columns lane and lane + 64, adding the partial tiles in
+        // partialIds (task) order starting from 0.0f.
+        const unsigned mcol = k * kSlice + lane;
 #pragma unroll 1
-        for (unsigned r = 0; r < valid; ++r) {
-            float lo = 0.0f, hi = 0.0f;
+        for (unsigned g = 0; g < 4; ++g) {
+            const Sw32ReduceRange red = a.m.reductions[task.reduceFirst + g];
+            const unsigned row0 = sw * 32 + g * 8;
+            if (row0 >= a.rows) continue;
+            const unsigned valid = min(8u, a.rows - row0);
 #pragma unroll 1
-            for (unsigned item = red.begin; item < red.end; ++item) {
-                const float* pr =
-                    a.partials + (std::size_t(a.m.partialIds[item]) * 8 + r) * Features + mcol;
-                lo += pr[0];
-                hi += pr[kWave];
+            for (unsigned r = 0; r < valid; ++r) {
+                float lo = 0.0f, hi = 0.0f;
+#pragma unroll 1
+                for (unsigned item = red.begin; item < red.end; ++item) {
+                    const float* pr =
+                        a.partials + (std::size_t(a.m.partialIds[item]) * 8 + r) * Features + mcol;
+                    lo += pr[0];
+                    hi += pr[kWave];
+                }
+                float* yr = a.y + std::size_t(row0 + r) * Features + mcol;
+                yr[0] = lo;
+                yr[kWave] = hi;
             }
-            float* yr = a.y + std::size_t(row0 + r) * Features + mcol;
-            yr[0] = lo;
-            yr[kWave] = hi;
         }
     }
 }
 
+// F128: four waves per SIMD; the 64 accumulators live in ordinary VGPRs and the kernel fits 128
+// registers.
+template <bool Wide>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) void spmmInt8Kernel128(
+    KernelArgs a) {
+    runTask<128, Wide>(a, xcdTask(blockIdx.x, a.m.taskCount));
+}
+
+// F256: both 128-feature slices of a task in one wave (128 accumulator registers, two waves per
+// SIMD). The task's A stream, scales and A table are read and built once for both slices; measured
+// on c3 this moves 18% fewer bytes (33.1 GB against 40.5 GB) and runs 8.6% faster than one wave
+// per (task, slice).
+template <bool Wide>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 8))) void spmmInt8Kernel256(
+    KernelArgs a) {
+    runTask<256, Wide>(a, xcdTask(blockIdx.x, a.m.taskCount));
+}
+
 template <unsigned Features>
 void launch(const KernelArgs& args, hipStream_t stream) {
-    const dim3 grid(args.m.taskCount, Features / kSlice);
     // Buffer addressing needs the packed X and the scales within 32-bit byte offsets, with room for
     // the padding sentinel to land out of range. TCC_SPMM_FORCE_WIDE selects the 64-bit instance
     // for any size (used by the tests).
     const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull ||
                       std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
-    if (wide)
-        hipLaunchKernelGGL((spmmInt8Kernel<Features, true>), grid, dim3(kWave), 0, stream, args);
-    else
-        hipLaunchKernelGGL((spmmInt8Kernel<Features, false>), grid, dim3(kWave), 0, stream, args);
+    const dim3 grid(args.m.taskCount, 1);
+    if constexpr (Features == 256) {
+        if (wide)
+            hipLaunchKernelGGL((spmmInt8Kernel256<true>), grid, dim3(kWave), 0, stream, args);
+        else
+            hipLaunchKernelGGL((spmmInt8Kernel256<false>), grid, dim3(kWave), 0, stream, args);
+    } else {
+        if (wide)
+            hipLaunchKernelGGL((spmmInt8Kernel128<true>), grid, dim3(kWave), 0, stream, args);
+        else
+            hipLaunchKernelGGL((spmmInt8Kernel128<false>), grid, dim3(kWave), 0, stream, args);
+    }
 }
 
 } // namespace
