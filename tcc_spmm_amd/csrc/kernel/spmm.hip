@@ -189,7 +189,8 @@ struct Stage {     // one panel, ready to compute
     u32x4 x[2];    // 16-byte tile L & 7 of the X row of slot L >> 3, per slice of the wave
 };
 
-// Stage 2 of one panel of kind G (row groups `groups` when G == kShared).
+// Stage 2 of one panel of kind G (row groups `groups` when G == kShared), with the X tiles of the
+// wave's S slices.
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned groups,
                                           unsigned lane, Stage& s) {
@@ -253,7 +254,7 @@ __device__ __forceinline__ void waveSync() {
 struct Lds {
     _Float16* table16; // [32 rows][8 slots] a' (f16 path)
     float* table32;    // [32 rows][8 slots] tf32(a) * 2^kShift (FP32 path)
-    u32x4* xtile;      // [8 slots][128 bytes] X slice rows of the panel
+    u32x4* xtile;      // [S][8 slots][128 bytes] X rows of the panel, one block per slice
     float* mant;       // [8 slots] scale mantissas of the panel
     unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
                           // the FP32 path, in the order found (a task has <= 384 panels)
