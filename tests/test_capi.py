@@ -29,6 +29,39 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_functions()) == set(SIGNATURES), "ctypes table out of sync with header"
 
 
+CXX_HEADERS = ("format/csr.h", "format/sw32.h", "format/int8_features.h", "spmm.h")
+
+
+def declared_cxx_functions():
+    """Names of the non-inline functions the C++ headers declare (the reference's surface)."""
+    names = set()
+    for h in CXX_HEADERS:
+        text = (ROOT / "include" / h).read_text()
+        text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^(?!\s*(?:static_assert|inline|return|#|struct|constexpr))[A-Za-z_][\w:<>]*\s+"
+                             r"([A-Za-z_]\w*)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_library_exports_the_cxx_surface():
+    import shutil
+    import subprocess
+    from tcc_spmm_amd._lib import LIB_PATH
+    names = declared_cxx_functions()
+    assert {"makeCanonicalCsr", "loadMatrixMarket", "convertCsrToSw32", "buildPanelTasks",
+            "quantizeFeaturesInt8", "packFeaturesInt8x16", "launchSpmmInt8"} <= set(names), names
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm is not installed")
+    out = subprocess.run([nm, "-DC", "--defined-only", str(LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {m.group(1) for m in re.finditer(r"\s[TW]\s+([A-Za-z_]\w*)\(", out)}
+    missing = [n for n in names if n not in exported]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+
+
 def test_version_and_error_reporting():
     from tcc_spmm_amd._lib import check, lib
     assert b"gfx950" in lib().tcc_version()
