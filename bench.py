@@ -12,7 +12,8 @@ Roofline: algorithmic bytes per launch B_alg = B_A + B_X + B_Y + B_P, computed f
   B_Y = 4 R F                                                    (Y written once)
   B_P = 64 F K                                                   (partial tiles written + read once)
 achieved = B_alg / kernel time, peak = 8.0e12 B/s. `traffic` (HBM bytes per launch: rocprofv3
-FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a 1 GiB copy) is read from
+FETCH_SIZE and WRITE_SIZE, each scaled by what the same counter reads for a 1 GiB device copy; the read
+request counters give the same read bytes within 0.2%) is read from
 profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present;
 `traffic_bw` is that traffic over the measured time (the memory system's actual load).
 
