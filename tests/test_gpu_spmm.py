@@ -71,16 +71,18 @@ def test_spmm_c1(oracle, gpu):
     assert_close(y, y_ref, "c1")
 
 
-def test_spmm_c2_full(oracle, gpu):
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_c2_full(oracle, gpu, feats):
+    """Every output row of c2 (8.4M nnz, split SWs included); F256 runs both slices in one wave."""
     csr = T.synth_csr("c2")
     fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
     assert fmt.partial_count > 0
-    x = features(csr.cols, 128, seed=102)
+    x = features(csr.cols, feats, seed=102 if feats == 128 else 202)
     packed, scale, _, sc, pk = gpu_prepare(x, gpu)
-    _, y = _run(fmt, packed, scale, 128, gpu)
+    _, y = _run(fmt, packed, scale, feats, gpu)
     y_ref = oracle.spmm_csr_f64(csr.rows, csr.row_offsets, csr.source_ids, csr.values, pk, sc,
                                 csr.cols)
-    assert_close(y, y_ref, "c2")
+    assert_close(y, y_ref, f"c2 F{feats}")
 
 
 def _sampled_windows(fmt, extra, count, seed):
