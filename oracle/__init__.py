@@ -41,6 +41,14 @@ class _OrcSw32(C.Structure):
     ]
 
 
+class _CheckStats(C.Structure):
+    _fields_ = [
+        ("checked", C.c_uint64), ("bad", C.c_uint64), ("relaxed", C.c_uint64),
+        ("maxErr", C.c_double), ("firstBad", C.c_uint64),
+        ("firstGot", C.c_double), ("firstWant", C.c_double), ("firstBound", C.c_double),
+    ]
+
+
 def _copy(ptr, count, dtype):
     dtype = np.dtype(dtype)
     if not count or not ptr:
@@ -87,6 +95,9 @@ class Oracle:
                                           C.c_void_p, C.c_void_p]
         so.orc_spmm_sw32_f32_mt.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p,
                                             C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_void_p]
+        so.orc_check_sw32_mt.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p, C.c_uint32,
+                                         C.c_void_p, C.c_double, C.c_double, C.c_double, C.c_int,
+                                         C.POINTER(_CheckStats), C.c_void_p]
 
     # ---- scalar helpers
     def tf32(self, v: float) -> float:
@@ -210,6 +221,30 @@ class OracleFormat:
                                                w.size, y.ctypes.data,
                                                ya.ctypes.data if with_abs else None)
         return (y, ya) if with_abs else y
+
+    def check_full(self, packed, scales, y, atol, rtol, cond=0.0, threads=8, with_ref=False):
+        """Compare every element of y ([rows, F] float32) with the double reference, SW by SW on
+        `threads` threads. Returns a dict of the counts (checked, bad, relaxed), max_err and the
+        first bad element (index, got, want, bound); with_ref also returns the reference."""
+        packed = np.ascontiguousarray(packed, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        y = np.ascontiguousarray(y, np.float32)
+        feats = packed.shape[1]
+        assert y.shape == (self.rows, feats)
+        ref = np.empty((self.rows, feats), np.float64) if with_ref else None
+        st = _CheckStats()
+        rc = self._orc.so.orc_check_sw32_mt(C.byref(self._f), packed.ctypes.data,
+                                            scales.ctypes.data, feats, y.ctypes.data, atol, rtol,
+                                            cond, int(threads), C.byref(st),
+                                            ref.ctypes.data if with_ref else None)
+        if rc:
+            raise OracleError(rc)
+        out = {"checked": st.checked, "bad": st.bad, "relaxed": st.relaxed,
+               "max_err": st.maxErr, "first_bad": None}
+        if st.bad:
+            out["first_bad"] = (divmod(int(st.firstBad), feats), st.firstGot, st.firstWant,
+                                st.firstBound)
+        return (out, ref) if with_ref else out
 
     def spmm_tasks_f32(self, packed, scales):
         packed = np.ascontiguousarray(packed, np.int8)

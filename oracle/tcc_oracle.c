@@ -15,6 +15,9 @@
  *   orc_tf32           -> known-answer bit patterns written from the rounding definition.
  *   orc_spmm_*         -> brute-force dense products on tiny inputs (numpy), CSR vs SW32 agreement,
  *                         split vs unsplit agreement.
+ *   orc_check_sw32_mt  -> its reference equals orc_spmm_sw32_f64_windows bitwise and the dense
+ *                         brute force; planted errors (beyond the bound, NaN, within the bound,
+ *                         within only the conditioning term) are flagged exactly.
  */
 #include "tcc_oracle.h"
 
@@ -644,4 +647,132 @@ int orc_spmm_sw32_f32_mt(const orc_sw32* fm, const int8_t* packedX, const float*
     }
     for (int t = 0; t < threads; ++t) pthread_join(th[t], NULL);
     return threads;
+}
+
+/* ---------------------------------------------------------------- full-size checker (threads) */
+typedef struct {
+    const orc_sw32* fm;
+    const int8_t* packedX;
+    const float* scales;
+    const float* y;
+    double* ref;
+    uint32_t features, swBegin, swEnd;
+    double atol, rtol, cond;
+    int nomem;
+    orc_check_stats st;
+} chk_args;
+
+/* Per SW: the reference rows in double in slot order (the accumulation of
+ * orc_spmm_sw32_f64_windows, so the values are bitwise the same), then the comparison. */
+static void* chk_worker(void* p) {
+    chk_args* a = (chk_args*)p;
+    const orc_sw32* fm = a->fm;
+    const uint32_t F = a->features;
+    double* acc = (double*)malloc((size_t)32 * F * sizeof(double));
+    double* mag = (double*)malloc((size_t)32 * F * sizeof(double));
+    double* xh = (double*)malloc((size_t)F * sizeof(double));
+    a->st.checked = a->st.bad = a->st.relaxed = 0;
+    a->st.maxErr = 0.0;
+    a->st.firstBad = UINT64_MAX;
+    a->nomem = !acc || !mag || !xh;
+    for (uint32_t sw = a->swBegin; sw < a->swEnd && !a->nomem; ++sw) {
+        memset(acc, 0, (size_t)32 * F * sizeof(double));
+        memset(mag, 0, (size_t)32 * F * sizeof(double));
+        for (size_t slot = (size_t)fm->windowOffsets[sw] * 8;
+             slot < (size_t)fm->windowOffsets[sw + 1] * 8; ++slot) {
+            uint32_t c = fm->sourceIds[slot];
+            if (c >= fm->cols) continue;
+            uint64_t md = fm->sourceMetadata[slot];
+            uint32_t mask = (uint32_t)md, base = (uint32_t)(md >> 32), k = 0;
+            for (uint32_t f = 0; f < F; ++f) xh[f] = (double)xhat(a->packedX, a->scales, c, f, F);
+            while (mask) {
+                uint32_t r = (uint32_t)__builtin_ctz(mask);
+                mask &= mask - 1;
+                double av = (double)orc_tf32(fm->values[base + k++]);
+                double* yr = acc + (size_t)r * F;
+                double* ya = mag + (size_t)r * F;
+                for (uint32_t f = 0; f < F; ++f) {
+                    double t = av * xh[f];
+                    yr[f] += t;
+                    ya[f] += fabs(t);
+                }
+            }
+        }
+        uint32_t rows = fm->rows - sw * 32 < 32 ? fm->rows - sw * 32 : 32;
+        for (uint32_t r = 0; r < rows; ++r) {
+            size_t row = (size_t)sw * 32 + r;
+            if (a->ref) memcpy(a->ref + row * F, acc + (size_t)r * F, (size_t)F * sizeof(double));
+            for (uint32_t f = 0; f < F; ++f) {
+                double want = acc[(size_t)r * F + f], got = (double)a->y[row * F + f];
+                double err = fabs(got - want);
+                if (err != err) err = INFINITY; /* NaN: never within a bound */
+                double plain = a->atol + a->rtol * fabs(want);
+                double bound = plain + a->cond * 0x1.0p-24 * mag[(size_t)r * F + f];
+                a->st.checked++;
+                if (err > a->st.maxErr) a->st.maxErr = err;
+                if (!(err <= bound)) {
+                    if (a->st.bad++ == 0) {
+                        a->st.firstBad = row * F + f;
+                        a->st.firstGot = got;
+                        a->st.firstWant = want;
+                        a->st.firstBound = bound;
+                    }
+                } else if (err > plain) {
+                    a->st.relaxed++;
+                }
+            }
+        }
+    }
+    free(acc);
+    free(mag);
+    free(xh);
+    return NULL;
+}
+
+int orc_check_sw32_mt(const orc_sw32* fm, const int8_t* packedX, const float* scales,
+                      uint32_t features, const float* y, double atol, double rtol, double cond,
+                      int threads, orc_check_stats* out, double* ref) {
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    uint32_t windows = (uint32_t)(fm->nWindowOffsets - 1);
+    pthread_t th[256];
+    chk_args* args = (chk_args*)calloc((size_t)threads, sizeof(chk_args));
+    if (!args) return ORC_NOMEM;
+    for (int t = 0; t < threads; ++t) {
+        chk_args* a = &args[t];
+        a->fm = fm;
+        a->packedX = packedX;
+        a->scales = scales;
+        a->y = y;
+        a->ref = ref;
+        a->features = features;
+        a->swBegin = (uint32_t)((uint64_t)windows * t / threads);
+        a->swEnd = (uint32_t)((uint64_t)windows * (t + 1) / threads);
+        a->atol = atol;
+        a->rtol = rtol;
+        a->cond = cond;
+        pthread_create(&th[t], NULL, chk_worker, a);
+    }
+    memset(out, 0, sizeof(*out));
+    out->firstBad = UINT64_MAX;
+    int nomem = 0;
+    for (int t = 0; t < threads; ++t) {
+        pthread_join(th[t], NULL);
+        nomem |= args[t].nomem;
+        const orc_check_stats* s = &args[t].st;
+        out->checked += s->checked;
+        out->bad += s->bad;
+        out->relaxed += s->relaxed;
+        if (s->maxErr > out->maxErr) out->maxErr = s->maxErr;
+        /* Threads cover increasing SW ranges: the first thread with a bad element has the
+         * smallest index. */
+        if (s->firstBad != UINT64_MAX && out->firstBad == UINT64_MAX) {
+            out->firstBad = s->firstBad;
+            out->firstGot = s->firstGot;
+            out->firstWant = s->firstWant;
+            out->firstBound = s->firstBound;
+        }
+    }
+    free(args);
+    return nomem ? ORC_NOMEM : ORC_OK;
 }

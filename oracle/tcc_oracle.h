@@ -77,12 +77,28 @@ void orc_spmm_sw32_f64(const orc_sw32* f, const int8_t* packedX, const float* sc
                        uint32_t features, double* y);
 
 /* As orc_spmm_sw32_f64 but only for the listed SWs: y has n*32 rows (rows past the matrix end stay
- * 0). Lets tests check sampled windows of configurations too large for a full CPU pass. */
+ * 0), with optional sum |terms| (below). */
 void orc_spmm_sw32_f64_windows(const orc_sw32* f, const int8_t* packedX, const float* scales,
                                uint32_t features, const uint32_t* windows, uint32_t n, double* y,
                                double* yabs);
 /* yabs (optional, same shape as y) receives sum |tf32(a) * xhat| per element: the scale of the FP32
  * summation error of any accumulation order (error <~ u * sum|terms| for a random walk). */
+
+/* Full-size comparison of a computed Y [rows][features] (float) against the double reference of
+ * orc_spmm_sw32_f64_windows, SW by SW on `threads` threads, without materialising the reference.
+ * An element passes when |y - ref| <= atol + rtol |ref| + cond * 2^-24 * sum|terms| (cond = 0: the
+ * plain bound). ref (optional, [rows][features] double) receives the reference itself. */
+typedef struct {
+    uint64_t checked;  /* elements compared */
+    uint64_t bad;      /* elements beyond the bound */
+    uint64_t relaxed;  /* elements within the bound only thanks to the cond term */
+    double maxErr;     /* max |y - ref| (NaN in y counts as +inf) */
+    uint64_t firstBad; /* flat index of the smallest bad element, UINT64_MAX when none */
+    double firstGot, firstWant, firstBound;
+} orc_check_stats;
+int orc_check_sw32_mt(const orc_sw32* f, const int8_t* packedX, const float* scales,
+                      uint32_t features, const float* y, double atol, double rtol, double cond,
+                      int threads, orc_check_stats* out, double* ref);
 
 /* Restatement of the kernel's task/partial/merge protocol in FP32 (spmm_kernel.cuh:228-282):
  * each task accumulates its panels in FP32 (slot order), unsplit tasks write Y, split tasks write

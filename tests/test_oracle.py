@@ -190,3 +190,48 @@ def test_spmm_split_tasks_merge_to_the_unsplit_sum(oracle):
     want = oracle.spmm_csr_f64(rows, csr.row_offsets, csr.source_ids, csr.values, pk, s, cols)
     err = np.abs(y - want)
     assert (err <= ATOL + RTOL * np.abs(want)).all()
+
+
+def test_full_checker_reference_and_verdicts(oracle):
+    """check_full recomputes the reference SW by SW on several threads: its reference must equal
+    the window oracle bitwise and the dense brute force, and its verdicts must flag exactly the
+    planted errors (the first one by index), NaN included."""
+    rows, cols, feats = 203, 300, 32                         # 7 SWs, the last with 11 rows
+    rng = np.random.default_rng(21)
+    dense, off, src, val = _random_csr(rng, rows, cols, 0.05)
+    x = rng.normal(0, 1, (cols, feats)).astype(np.float32)
+    q, s = oracle.quantize(x)
+    pk = oracle.pack16(q)
+    fmt = oracle.sw32(rows, cols, off, src, val)
+    a_t = np.vectorize(tf32_exact, otypes=[np.float64])(dense.astype(np.float64))
+    want = a_t @ _xhat_independent(q, s)
+    windows = np.arange((rows + 31) // 32, dtype=np.uint32)
+    win, mag = fmt.spmm_windows_f64(pk, s, windows, with_abs=True)
+    win, mag = win[:rows], mag[:rows]
+
+    y = want.astype(np.float32)
+    st, ref = fmt.check_full(pk, s, y, ATOL, RTOL, threads=3, with_ref=True)
+    assert np.array_equal(ref.view(np.uint64), win.view(np.uint64))
+    assert np.allclose(ref, want, rtol=1e-12, atol=1e-12)
+    assert (st["checked"], st["bad"], st["relaxed"], st["first_bad"]) == (rows * feats, 0, 0, None)
+
+    plain = ATOL + RTOL * np.abs(ref)
+    bad = y.copy()
+    bad[150, 7] = np.float32(ref[150, 7] + 2 * plain[150, 7])   # SW 4 (third thread)
+    bad[40, 3] = np.float32(ref[40, 3] - 3 * plain[40, 3])      # SW 1 (first thread): the first
+    bad[200, 31] = np.nan                                       # tail SW
+    bad[90, 0] = np.float32(ref[90, 0] + 0.5 * plain[90, 0])    # within the bound
+    st = fmt.check_full(pk, s, bad, ATOL, RTOL, threads=3)
+    assert st["bad"] == 3 and st["max_err"] == np.inf
+    (r, f), got, wnt, bound = st["first_bad"]
+    assert (r, f) == (40, 3) and got == float(bad[40, 3]) and wnt == ref[40, 3]
+    assert bound == plain[40, 3]
+
+    # The conditioning term: an error beyond the plain bound but within cond * 2^-24 * sum|terms|.
+    cond = 1e-2 * 2.0 ** 24
+    r, f = np.unravel_index(np.argmax(mag), mag.shape)
+    loose = y.copy()
+    loose[r, f] = np.float32(ref[r, f] + plain[r, f] + 0.5 * 1e-2 * mag[r, f])
+    assert fmt.check_full(pk, s, loose, ATOL, RTOL, threads=2)["bad"] == 1
+    st = fmt.check_full(pk, s, loose, ATOL, RTOL, cond=cond, threads=2)
+    assert (st["bad"], st["relaxed"]) == (0, 1)
