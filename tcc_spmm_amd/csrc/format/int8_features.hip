@@ -27,7 +27,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
     const float* __restrict__ x, std::int8_t* __restrict__ q, float* __restrict__ scale,
     unsigned sources, unsigned features) {
     const unsigned lane = threadIdx.x & (kWave - 1);
-    const unsigned row = blockIdx.x * kRowsPerBlock + (threadIdx.x / kWave);
+    const std::size_t row = std::size_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x / kWave);
     if (row >= sources) return;
     const float* xr = x + std::size_t(row) * features;
     float m = 0.0f;
@@ -179,7 +179,7 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
             }
         }
     } else {
-        const unsigned blocks = (sources + kRowsPerBlock - 1) / kRowsPerBlock;
+        const unsigned blocks = unsigned((std::size_t(sources) + kRowsPerBlock - 1) / kRowsPerBlock);
         hipLaunchKernelGGL(quantizeRows, dim3(blocks), dim3(kWave * kRowsPerBlock), 0, stream, x,
                            q, scale, sources, features);
     }

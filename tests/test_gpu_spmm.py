@@ -152,23 +152,28 @@ def test_spmm_c3_full(oracle, gpu, c3_case, feats):
     print(f"c3 F{feats}: {st['checked']} elements, max err {st['max_err']:.3g}")
 
 
-def test_stream_reuse_and_overwrite(oracle, gpu):
-    import torch
-    from tcc_spmm_amd.device import TorchDeviceMatrix
-    # Split-heavy small case: two split SWs plus ordinary ones.
+def _split_heavy_csr():
+    """t4000_40_9 with rows 5, 40 and 41 referencing all 4,000 sources: two split SWs (500 panels
+    each) among ordinary ones."""
     csr = T.synth_csr("t4000_40_9")
     rng = np.random.default_rng(4)
     off = csr.row_offsets.astype(np.int64)
     src, val = csr.source_ids, csr.values
-    heavy = np.arange(0, csr.cols, dtype=np.uint32)  # 4000 sources: 500 panels -> split SW
+    heavy = np.arange(0, csr.cols, dtype=np.uint32)
     rows_cols = [src[off[r]:off[r + 1]] for r in range(csr.rows)]
     rows_vals = [val[off[r]:off[r + 1]] for r in range(csr.rows)]
     for r in (5, 40, 41):
         rows_cols[r] = heavy
         rows_vals[r] = rng.uniform(0.1, 1.0, heavy.size).astype(np.float32)
     new_off = np.concatenate([[0], np.cumsum([len(c) for c in rows_cols])]).astype(np.uint32)
-    c2 = T.make_canonical_csr(csr.rows, csr.cols, new_off, np.concatenate(rows_cols),
-                              np.concatenate(rows_vals))
+    return T.make_canonical_csr(csr.rows, csr.cols, new_off, np.concatenate(rows_cols),
+                                np.concatenate(rows_vals))
+
+
+def test_stream_reuse_and_overwrite(oracle, gpu):
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    c2 = _split_heavy_csr()
     fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
     assert fmt.partial_count > 0
     x = features(c2.cols, 256, seed=77)
@@ -189,6 +194,36 @@ def test_stream_reuse_and_overwrite(oracle, gpu):
         assert np.array_equal(y.cpu().numpy().view(np.uint32), y0.view(np.uint32))
     y_ref = oracle.sw32(c2.rows, c2.cols, *c2.views()).spmm_f64(pk, sc)
     assert_close(y0, y_ref, "stream reuse")
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_concurrent_launches_with_separate_workspaces(oracle, gpu, feats):
+    """Launches on two streams at once, each with its own workspace (the reference's contract for
+    concurrent use, include/spmm.cuh:8-9), four back to back per stream with no host wait: every
+    output matches the serial result bitwise and both counter arrays end at zero."""
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    c2 = _split_heavy_csr()
+    fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
+    x = features(c2.cols, feats, seed=78)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    _, y_serial = _run(fmt, packed, scale, feats, gpu)
+    dms = [TorchDeviceMatrix(fmt, feats, device=gpu) for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[torch.full((c2.rows, feats), float("nan"), device=gpu) for _ in range(4)]
+            for _ in range(2)]
+    torch.cuda.synchronize()
+    for it in range(4):
+        for k in range(2):
+            with torch.cuda.stream(streams[k]):
+                dms[k].spmm(packed, scale, outs[k][it], stream=streams[k])
+    torch.cuda.synchronize()
+    for k in range(2):
+        assert int(dms[k].counters.abs().sum()) == 0
+        for y in outs[k]:
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), y_serial.view(np.uint32))
+    y_ref = oracle.sw32(c2.rows, c2.cols, *c2.views()).spmm_f64(pk, sc)
+    assert_close(y_serial, y_ref, f"concurrent F{feats}")
 
 
 def test_native_device_matrix_matches_torch_upload(gpu):
@@ -298,6 +333,57 @@ def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
         assert np.array_equal(y_wide.view(np.uint32), y_narrow.view(np.uint32)), case
         y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
         assert_close(y_wide, y_ref, f"{case} F{feats} wide")
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_wide_addressing_at_real_size(oracle, gpu, feats):
+    """Packed X of more than 4 GiB (cols * F > 2^32 - 256): the launch takes the 64-bit-addressing
+    instance on its own. Sources are drawn so that many byte offsets exceed 2^32, two rows make
+    split SWs, and X is generated on the GPU (17 GB of FP32 features). Quantize and pack are
+    checked bit-exactly on every referenced row, Y on every element (the oracle runs on the
+    referenced rows only, renumbered in order, which leaves every sum unchanged)."""
+    import torch
+    from tcc_spmm_amd.device import pack_features_int8x16, quantize_features_int8
+    cols = (1 << 32) // feats + 65_537
+    assert cols * feats > 0xFFFFFF00
+    rows, rng = 2_053, np.random.default_rng(feats)
+    top = (1 << 32) // feats                                  # first source past 32-bit offsets
+    lists = []
+    for r in range(rows):
+        if r in (7, 1_900):                                   # > 384 panels: split SWs
+            picks = np.concatenate([rng.choice(top, 1_600, replace=False),
+                                    top + rng.choice(cols - top, 1_600, replace=False)])
+        else:
+            picks = np.concatenate([rng.integers(0, cols, 8), rng.integers(top, cols, 8),
+                                    [cols - 1]])
+        lists.append(np.unique(picks).astype(np.uint32))
+    off = np.concatenate([[0], np.cumsum([len(c) for c in lists])]).astype(np.uint32)
+    src = np.concatenate(lists)
+    val = rng.uniform(-1, 1, src.size).astype(np.float32)
+    csr = T.make_canonical_csr(rows, cols, off, src, val)
+    fmt = T.convert_csr_to_sw32(rows, cols, csr)
+    assert fmt.partial_count > 0
+
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(1000 + feats)
+    x = torch.randn((cols, feats), generator=gen, device=gpu)
+    q, scale = quantize_features_int8(x)
+    packed = pack_features_int8x16(q)
+    used = np.unique(csr.source_ids)
+    assert int(used.max()) * feats >= 1 << 32
+    idx = torch.from_numpy(used.astype(np.int64)).to(gpu)
+    x_u = x.index_select(0, idx).cpu().numpy()
+    q_u = q.index_select(0, idx).cpu().numpy()
+    sc_u = scale.index_select(0, idx).cpu().numpy()
+    pk_u = packed.index_select(0, idx).cpu().numpy()
+    del x, q
+    torch.cuda.empty_cache()
+    check_features(oracle, x_u, q_u, sc_u, pk_u)
+
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    renumbered = np.searchsorted(used, csr.source_ids).astype(np.uint32)
+    ofmt = oracle.sw32(rows, used.size, csr.row_offsets, renumbered, csr.values)
+    _check_full(ofmt, y, pk_u, sc_u, f"wide F{feats}")
 
 
 @pytest.mark.parametrize("shape,offset", [
