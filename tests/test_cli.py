@@ -128,6 +128,10 @@ def test_config_run_with_normal_features_matches_oracle(oracle, tmp_path):
     rec = json.loads(js.read_text())
     assert rec["source"] == "config:c1" and rec["x"] == "normal:7" and rec["nnz"] == 65536
     assert rec["warmup"] == 10 and rec["iterations"] == 10
+    # The harness's GB/s uses the same byte count as bench.py.
+    import bench
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    assert rec["algorithmic_bytes"] == bench.algorithmic_bytes(fmt, csr.source_ids, 128)["B_alg"]
 
 
 @pytest.mark.gpu
