@@ -1,7 +1,7 @@
 """bench.py's accounting and argument handling (host only).
 
-The roofline numerator is checked against the byte sizes of the arrays the kernel actually reads, so
-a dropped or double-counted term in the formula fails here.
+The roofline numerator is checked against the byte sizes of the uploaded format arrays (every array but
+windowOffsets, each counted once), so a dropped or double-counted term in the formula fails here.
 """
 import subprocess
 import sys
@@ -26,7 +26,7 @@ def _split_format():
     return csr, T.convert_csr_to_sw32(rows, cols, csr)
 
 
-def test_algorithmic_bytes_equal_the_arrays_the_kernel_reads():
+def test_algorithmic_bytes_equal_the_uploaded_arrays():
     csr, fmt = _split_format()
     a = fmt.arrays()
     assert fmt.partial_count > 0
