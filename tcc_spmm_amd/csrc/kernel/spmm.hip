@@ -99,7 +99,6 @@ struct Meta {        // one panel
     unsigned id;     // lane L: source of slot L & 7
     unsigned mask;   // lane L: row mask of slot L & 7
     unsigned base;   // lane L: value base of slot L & 7
-    unsigned gather; // lane L: source of slot L >> 3 (the row this lane gathers)
 };
 
 template <bool Wide>
@@ -133,8 +132,7 @@ struct Loader<false> {
     __device__ Meta meta8(unsigned panel, unsigned lane) const {
         const int off = int((panel - first) * 32u);
         const auto md = __builtin_amdgcn_raw_buffer_load_b64(meta, (lane & 7) * 8, 2 * off, kNt);
-        return {__builtin_amdgcn_raw_buffer_load_b32(ids, (lane & 7) * 4, off, kNt), md[0], md[1],
-                __builtin_amdgcn_raw_buffer_load_b32(ids, (lane >> 3) * 4, off, kNt)};
+        return {__builtin_amdgcn_raw_buffer_load_b32(ids, (lane & 7) * 4, off, kNt), md[0], md[1]};
     }
     __device__ float scale(unsigned src) const {
         return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(scales, src * 4u, 0, 0));
@@ -164,8 +162,7 @@ struct Loader<true> {
         const std::uint64_t md =
             __builtin_nontemporal_load(a->m.sourceMetadata + first + (lane & 7));
         return {__builtin_nontemporal_load(a->m.sourceIds + first + (lane & 7)), unsigned(md),
-                unsigned(md >> 32),
-                __builtin_nontemporal_load(a->m.sourceIds + first + (lane >> 3))};
+                unsigned(md >> 32)};
     }
     __device__ float scale(unsigned src) const { return a->scales[min(src, a->cols - 1)]; }
     // values[idx] (absent entries are masked by Stage::bits).
@@ -213,8 +210,11 @@ __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned 
             s.v[j] = ld.value(idx, present);
         }
     }
+    // Lane L gathers slot L >> 3's row, whose source lane L >> 3 holds: a cross-lane permute instead
+    // of a second sourceIds load (one vector memory instruction fewer per panel, 2% at c3 F128).
+    const unsigned gather = unsigned(__builtin_amdgcn_ds_bpermute(int((lane >> 3) * 4), int(m.id)));
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) s.x[k] = ld.tile(m.gather, lane, k);
+    for (unsigned k = 0; k < S; ++k) s.x[k] = ld.tile(gather, lane, k);
 }
 
 // ------------------------------------------------------------------------------------------------
