@@ -28,9 +28,9 @@
 // range (or whose scale is subnormal) takes an FP32 path with the same products:
 // v_mfma_f32_32x32x2_f32 on tf32(a) * 2^kShift and the TF32 features.
 //
-// The panels are walked by a three-stage software pipeline (metadata two panels ahead; scales, A
-// values and X one panel ahead) whose memory operations are identical on every path. F128 runs four
-// waves per SIMD (128 registers each, accumulators included), F256 two (192 registers).
+// The panels are walked by a software pipeline (metadata two panels ahead, in pairs of panels at
+// F128; A values and X one panel ahead) whose memory operations are identical on every path. F128
+// runs four waves per SIMD (128 registers each, accumulators included), F256 two (192 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes, per slice, an agent-scope
@@ -101,6 +101,23 @@ struct Meta {        // one panel
     unsigned base;   // lane L: value base of slot L & 7
 };
 
+// Lane L's value of v from lane srcLane (LDS crossbar, no memory access).
+__device__ __forceinline__ unsigned lanePermute(unsigned v, unsigned srcLane) {
+    return unsigned(__builtin_amdgcn_ds_bpermute(int(srcLane * 4), int(v)));
+}
+
+// Metadata of panels q and q + 1 loaded together (F128 walk): lane L holds slot L & 7 of panel
+// q + ((L >> 3) & 1), lanes 16..63 repeating lanes 0..15.
+struct MetaPair {
+    unsigned id, mask, base;
+};
+
+// Panel q + e (e = 0, 1) of a pair, in the per-panel lane layout.
+__device__ __forceinline__ Meta pairPanel(const MetaPair& m, unsigned e, unsigned lane) {
+    const unsigned own = 8 * e + (lane & 7);
+    return {lanePermute(m.id, own), lanePermute(m.mask, own), lanePermute(m.base, own)};
+}
+
 template <bool Wide>
 struct Loader;
 
@@ -134,6 +151,12 @@ struct Loader<false> {
         const auto md = __builtin_amdgcn_raw_buffer_load_b64(meta, (lane & 7) * 8, 2 * off, kNt);
         return {__builtin_amdgcn_raw_buffer_load_b32(ids, (lane & 7) * 4, off, kNt), md[0], md[1]};
     }
+    // Panels q and q + 1, each clamped to `last`: one load per array for both.
+    __device__ MetaPair meta2(unsigned q, unsigned last, unsigned lane) const {
+        const unsigned off = (min(q + ((lane >> 3) & 1u), last) - first) * 32u + (lane & 7) * 4;
+        const auto md = __builtin_amdgcn_raw_buffer_load_b64(meta, 2 * off, 0, kNt);
+        return {__builtin_amdgcn_raw_buffer_load_b32(ids, off, 0, kNt), md[0], md[1]};
+    }
     __device__ float scale(unsigned src) const {
         return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(scales, src * 4u, 0, 0));
     }
@@ -164,6 +187,11 @@ struct Loader<true> {
         return {__builtin_nontemporal_load(a->m.sourceIds + first + (lane & 7)), unsigned(md),
                 unsigned(md >> 32)};
     }
+    __device__ MetaPair meta2(unsigned q, unsigned last, unsigned lane) const {
+        const std::size_t s = std::size_t(min(q + ((lane >> 3) & 1u), last)) * 8 + (lane & 7);
+        const std::uint64_t md = __builtin_nontemporal_load(a->m.sourceMetadata + s);
+        return {__builtin_nontemporal_load(a->m.sourceIds + s), unsigned(md), unsigned(md >> 32)};
+    }
     __device__ float scale(unsigned src) const { return a->scales[min(src, a->cols - 1)]; }
     // values[idx] (absent entries are masked by Stage::bits).
     __device__ float value(unsigned idx, bool) const {
@@ -187,13 +215,13 @@ struct Stage {     // one panel, ready to compute
 };
 
 // Stage 2 of one panel of kind G (row groups `groups` when G == kShared), with the X tiles of the
-// wave's S slices.
-template <unsigned G, unsigned S, class Ld>
+// wave's S slices; the scale too unless the caller loads it (LoadScale false).
+template <unsigned G, unsigned S, class Ld, bool LoadScale = true>
 __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned groups,
                                           unsigned lane, Stage& s) {
     // Padding slots (source UINT32_MAX, metadata 0) have an empty row mask; their scale and X tile
     // read 0 (narrow) or a clamped row (wide), multiplied by A entries that are all 0.
-    s.scale = ld.scale(m.id);
+    if constexpr (LoadScale) s.scale = ld.scale(m.id);
     s.bits = 0;
     constexpr unsigned kCount = G < 4 ? 1 : 4;
 #pragma unroll
@@ -212,7 +240,7 @@ __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned 
     }
     // Lane L gathers slot L >> 3's row, whose source lane L >> 3 holds: a cross-lane permute instead
     // of a second sourceIds load (one vector memory instruction fewer per panel, 2% at c3 F128).
-    const unsigned gather = unsigned(__builtin_amdgcn_ds_bpermute(int((lane >> 3) * 4), int(m.id)));
+    const unsigned gather = lanePermute(m.id, lane >> 3);
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) s.x[k] = ld.tile(gather, lane, k);
 }
@@ -398,8 +426,14 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
     }
 }
 
-// The panels [lo, hi) of kind G, three-stage pipelined, two panels per iteration with the odd one
-// after the loop (a single exit keeps the accumulators in place).
+// The panels [lo, hi) of kind G, pipelined, two panels per iteration with the odd one after the
+// loop (a single exit keeps the accumulators in place). Panel indices past the end repeat the last
+// panel (harmless loads, never computed).
+//
+// F128 (S == 1) loads the metadata, sourceIds and scales of two panels with one instruction each, one
+// iteration ahead, and hands each panel its slots by cross-lane permutes: per panel that is one and
+// a half vector memory instructions fewer (c3: 3.51 -> 3.44 ms). F256, at two waves per SIMD, keeps
+// one metadata load per panel two panels ahead (the permutes' latency cost it 2%).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4 * S]) {
@@ -413,42 +447,63 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
     }
     BucketCursor cur{w.offsets, 5, w.offsets[6]};
     auto groupsAt = [&](unsigned p) { return G < 4 ? (1u << G) : cur.groups(p); };
-    // Panel indices past the end repeat the last panel (harmless loads, never computed).
     const unsigned last = hi - 1;
-    const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
-    Stage sa, sb;
-    unsigned ga = groupsAt(lo);
-    loadStage<G, S>(ld, ld.meta8(lo, lane), ga, lane, sa);
-    unsigned g1 = groupsAt(p1), g2 = groupsAt(p2), gb = 0;
-    // The loop expects m1's loads to be older than m2's (waits are counted in issue order).
-    Meta m1 = ld.meta8(p1, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    Meta m2 = ld.meta8(p2, lane);
-    unsigned p = p2;
     const unsigned pairs = n / 2;
+    Stage sa, sb;
+    unsigned ga = groupsAt(lo), gb = 0;
+    loadStage<G, S>(ld, ld.meta8(lo, lane), ga, lane, sa);
+    if constexpr (S == 1) {
+        MetaPair pair = ld.meta2(min(lo + 1, last), last, lane); // panels lo + 1, lo + 2
 #pragma unroll 1
-    for (unsigned k = 0; k < pairs; ++k) {
-        // Panels lo + 2k (in sa) and lo + 2k + 1; stage 2 one panel ahead, stage 1 two.
-        gb = g1;
-        loadStage<G, S>(ld, m1, gb, lane, sb);
-        p = min(p + 1, last);
-        m1 = m2;
-        g1 = g2;
-        g2 = groupsAt(p);
-        m2 = ld.meta8(p, lane);
-        // Issue this half's loads before any use of the previous half's: the vmcnt counter is in
-        // order, so computing first would wait for loads issued only half an iteration ago.
+        for (unsigned k = 0; k < pairs; ++k) {
+            // Computes panels lo + 2k (in sa) and lo + 2k + 1; loads the pair after next.
+            const MetaPair next = ld.meta2(min(lo + 2 * k + 3, last), last, lane);
+            const float sc = ld.scale(pair.id); // both panels' scales, laid out as `pair`
+            gb = groupsAt(min(lo + 2 * k + 1, last));
+            loadStage<G, S, Ld, false>(ld, pairPanel(pair, 0, lane), gb, lane, sb);
+            // Issue this half's loads before any use of the previous half's: the vmcnt counter
+            // is in order, so computing first would wait for loads issued only half an
+            // iteration ago.
+            __builtin_amdgcn_sched_barrier(0);
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
+            ga = groupsAt(min(lo + 2 * k + 2, last));
+            loadStage<G, S, Ld, false>(ld, pairPanel(pair, 1, lane), ga, lane, sa);
+            __builtin_amdgcn_sched_barrier(0);
+            sb.scale = __uint_as_float(lanePermute(__float_as_uint(sc), lane & 7));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
+            sa.scale = __uint_as_float(lanePermute(__float_as_uint(sc), 8 + (lane & 7)));
+            pair = next;
+        }
+    } else {
+        const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
+        unsigned g1 = groupsAt(p1), g2 = groupsAt(p2);
+        // The loop expects m1's loads to be older than m2's (waits are counted in issue order).
+        Meta m1 = ld.meta8(p1, lane);
         __builtin_amdgcn_sched_barrier(0);
-        flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
-        ga = g1;
-        loadStage<G, S>(ld, m1, ga, lane, sa);
-        p = min(p + 1, last);
-        m1 = m2;
-        g1 = g2;
-        g2 = groupsAt(p);
-        m2 = ld.meta8(p, lane);
-        __builtin_amdgcn_sched_barrier(0);
-        flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
+        Meta m2 = ld.meta8(p2, lane);
+        unsigned p = p2;
+#pragma unroll 1
+        for (unsigned k = 0; k < pairs; ++k) {
+            // Panels lo + 2k (in sa) and lo + 2k + 1; stage 2 one panel ahead, metadata two.
+            gb = g1;
+            loadStage<G, S>(ld, m1, gb, lane, sb);
+            p = min(p + 1, last);
+            m1 = m2;
+            g1 = g2;
+            g2 = groupsAt(p);
+            m2 = ld.meta8(p, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
+            ga = g1;
+            loadStage<G, S>(ld, m1, ga, lane, sa);
+            p = min(p + 1, last);
+            m1 = m2;
+            g1 = g2;
+            g2 = groupsAt(p);
+            m2 = ld.meta8(p, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
+        }
     }
     if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
 }
