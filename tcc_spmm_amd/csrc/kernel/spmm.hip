@@ -432,8 +432,8 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 //
 // F128 (S == 1) loads the metadata, sourceIds and scales of two panels with one instruction each, one
 // iteration ahead, and hands each panel its slots by cross-lane permutes: per panel that is one and
-// a half vector memory instructions fewer (c3: 3.51 -> 3.44 ms). F256, at two waves per SIMD, keeps
-// one metadata load per panel two panels ahead (the permutes' latency cost it 2%).
+// a half vector memory instructions fewer (c3: 3.51 -> 3.43 ms). F256, at two waves per SIMD, keeps
+// one metadata load per panel two panels ahead (the permutes' latency cost it 1-2%).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4 * S]) {
@@ -454,25 +454,29 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
     loadStage<G, S>(ld, ld.meta8(lo, lane), ga, lane, sa);
     if constexpr (S == 1) {
         MetaPair pair = ld.meta2(min(lo + 1, last), last, lane); // panels lo + 1, lo + 2
+        // Each panel's permutes run half an iteration before its loads need them.
+        Meta mFirst = pairPanel(pair, 0, lane);
 #pragma unroll 1
         for (unsigned k = 0; k < pairs; ++k) {
             // Computes panels lo + 2k (in sa) and lo + 2k + 1; loads the pair after next.
             const MetaPair next = ld.meta2(min(lo + 2 * k + 3, last), last, lane);
             const float sc = ld.scale(pair.id); // both panels' scales, laid out as `pair`
             gb = groupsAt(min(lo + 2 * k + 1, last));
-            loadStage<G, S, Ld, false>(ld, pairPanel(pair, 0, lane), gb, lane, sb);
+            loadStage<G, S, Ld, false>(ld, mFirst, gb, lane, sb);
+            const Meta mSecond = pairPanel(pair, 1, lane);
             // Issue this half's loads before any use of the previous half's: the vmcnt counter
             // is in order, so computing first would wait for loads issued only half an
             // iteration ago.
             __builtin_amdgcn_sched_barrier(0);
             flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
             ga = groupsAt(min(lo + 2 * k + 2, last));
-            loadStage<G, S, Ld, false>(ld, pairPanel(pair, 1, lane), ga, lane, sa);
+            loadStage<G, S, Ld, false>(ld, mSecond, ga, lane, sa);
             __builtin_amdgcn_sched_barrier(0);
             sb.scale = __uint_as_float(lanePermute(__float_as_uint(sc), lane & 7));
             flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
             sa.scale = __uint_as_float(lanePermute(__float_as_uint(sc), 8 + (lane & 7)));
             pair = next;
+            mFirst = pairPanel(pair, 0, lane);
         }
     } else {
         const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
