@@ -112,10 +112,17 @@ struct MetaPair {
     unsigned id, mask, base;
 };
 
-// Panel q + e (e = 0, 1) of a pair, in the per-panel lane layout.
-__device__ __forceinline__ Meta pairPanel(const MetaPair& m, unsigned e, unsigned lane) {
-    const unsigned own = 8 * e + (lane & 7);
-    return {lanePermute(m.id, own), lanePermute(m.mask, own), lanePermute(m.base, own)};
+// Panel q + E (E = 0, 1) of a pair, in the per-panel lane layout: within each 16-lane DPP row the
+// half holding the other panel takes the wanted half's values (row_shr:8 into lanes 8..15 for
+// E = 0, row_shl:8 into lanes 0..7 for E = 1), one VALU move per field and no LDS round trip.
+template <unsigned E>
+__device__ __forceinline__ unsigned pairHalf(unsigned v) {
+    return E == 0 ? unsigned(__builtin_amdgcn_update_dpp(int(v), int(v), 0x118, 0xF, 0xC, false))
+                  : unsigned(__builtin_amdgcn_update_dpp(int(v), int(v), 0x108, 0xF, 0x3, false));
+}
+template <unsigned E>
+__device__ __forceinline__ Meta pairPanel(const MetaPair& m) {
+    return {pairHalf<E>(m.id), pairHalf<E>(m.mask), pairHalf<E>(m.base)};
 }
 
 template <bool Wide>
@@ -431,9 +438,9 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 // panel (harmless loads, never computed).
 //
 // F128 (S == 1) loads the metadata, sourceIds and scales of two panels with one instruction each, one
-// iteration ahead, and hands each panel its slots by cross-lane permutes: per panel that is one and
+// iteration ahead, and hands each panel its slots by DPP row shifts: per panel that is one and
 // a half vector memory instructions fewer (c3: 3.51 -> 3.43 ms). F256, at two waves per SIMD, keeps
-// one metadata load per panel two panels ahead (the permutes' latency cost it 1-2%).
+// one metadata load per panel two panels ahead (pairs cost it 0.5-2% in every form tried).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4 * S]) {
@@ -454,8 +461,8 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
     loadStage<G, S>(ld, ld.meta8(lo, lane), ga, lane, sa);
     if constexpr (S == 1) {
         MetaPair pair = ld.meta2(min(lo + 1, last), last, lane); // panels lo + 1, lo + 2
-        // Each panel's permutes run half an iteration before its loads need them.
-        Meta mFirst = pairPanel(pair, 0, lane);
+        // Each panel's row shifts run half an iteration before its loads need them.
+        Meta mFirst = pairPanel<0>(pair);
 #pragma unroll 1
         for (unsigned k = 0; k < pairs; ++k) {
             // Computes panels lo + 2k (in sa) and lo + 2k + 1; loads the pair after next.
@@ -463,7 +470,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             const float sc = ld.scale(pair.id); // both panels' scales, laid out as `pair`
             gb = groupsAt(min(lo + 2 * k + 1, last));
             loadStage<G, S, Ld, false>(ld, mFirst, gb, lane, sb);
-            const Meta mSecond = pairPanel(pair, 1, lane);
+            const Meta mSecond = pairPanel<1>(pair);
             // Issue this half's loads before any use of the previous half's: the vmcnt counter
             // is in order, so computing first would wait for loads issued only half an
             // iteration ago.
@@ -472,11 +479,11 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             ga = groupsAt(min(lo + 2 * k + 2, last));
             loadStage<G, S, Ld, false>(ld, mSecond, ga, lane, sa);
             __builtin_amdgcn_sched_barrier(0);
-            sb.scale = __uint_as_float(lanePermute(__float_as_uint(sc), lane & 7));
+            sb.scale = __uint_as_float(pairHalf<0>(__float_as_uint(sc)));
             flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
-            sa.scale = __uint_as_float(lanePermute(__float_as_uint(sc), 8 + (lane & 7)));
+            sa.scale = __uint_as_float(pairHalf<1>(__float_as_uint(sc)));
             pair = next;
-            mFirst = pairPanel(pair, 0, lane);
+            mFirst = pairPanel<0>(pair);
         }
     } else {
         const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
