@@ -439,7 +439,7 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 //
 // F128 (S == 1) loads the metadata, sourceIds and scales of two panels with one instruction each, one
 // iteration ahead, and hands each panel its slots by DPP row shifts: per panel that is one and
-// a half vector memory instructions fewer (c3: 3.51 -> 3.43 ms). F256, at two waves per SIMD, keeps
+// a half vector memory instructions fewer (c3: 3.51 -> 3.39 ms). F256, at two waves per SIMD, keeps
 // one metadata load per panel two panels ahead (pairs cost it 0.5-2% in every form tried).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
