@@ -53,11 +53,28 @@ def _compile(src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
+def check_kernel_asm(src: pathlib.Path = CSRC / "kernel" / "spmm.hip") -> None:
+    """Assemble the SpMM kernels for gfx950 and refuse them if they spill to scratch or read an
+    MFMA result too early (tcc_spmm_amd/asm_check.py explains why the build checks this)."""
+    from . import asm_check
+    out = BUILD / "spmm-gfx950.s"
+    cmd = [str(ROCM / "bin" / "hipcc"), *HIP_FLAGS, "--cuda-device-only", "-S", str(src), "-o",
+           str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"assembly listing failed: {shlex.join(cmd)}\n{res.stderr}")
+    problems = asm_check.check(out.read_text())
+    if problems:
+        raise RuntimeError("SpMM kernel assembly check failed:\n  " + "\n  ".join(problems))
+
+
 def build(verbose: bool = False) -> pathlib.Path:
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        asm = pool.submit(check_kernel_asm)
         objs = list(pool.map(_compile, srcs))
+        asm.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [str(ROCM / "bin" / "hipcc"), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp),
            *map(str, objs), "-lpthread"]

@@ -19,14 +19,17 @@
 //
 // Exact TF32 products in f16. With the slot's scale written s = m * 2^e (m in [0.5, 1)),
 // x_hat = tf32(fp32(q * s)) = tf32(fp32(q * m)) * 2^e exactly whenever s is normal, and
-// x~ = tf32(fp32(q * m)) lies in [0.5, 127]: eleven significant bits in f16's normal range. The
-// factor 2^e moves into B: a' = tf32(a) * 2^(e + kShift), also eleven bits, exact in f16 when in
-// f16's normal range. The MFMA sums exact products a' * x~ = 2^kShift * tf32(a) * x_hat in FP32,
-// so any accumulation order reproduces the reference's products; the task ends by scaling with
-// 2^-kShift. TF32 rounding (ties away from zero) is "add 0x1000 to the FP32 pattern, truncate",
-// and the truncation is the round-toward-zero f16 conversion. A panel whose a' leaves f16's normal
-// range (or whose scale is subnormal) takes an FP32 path with the same products:
-// v_mfma_f32_32x32x2_f32 on tf32(a) * 2^kShift and the TF32 features.
+// x~ = tf32(fp32(q * m)) lies in [0.5, 127]: eleven significant bits. The factor 2^e moves into B:
+// a' = tf32(a) * 2^(e + kShift), also eleven bits, exact in f16 when in f16's normal range (kShift
+// keeps the usual A values there). A takes x~ * 2^-kXShift (kXShift = kShift + 1), which stays in
+// [2^-12, 2^-4): still eleven bits in f16's normal range. The MFMA thus sums exact products
+// a' * x~ * 2^-kXShift = tf32(a) * x_hat / 2 in FP32, so any accumulation order reproduces the
+// reference's products, and the task doubles its accumulators at the end (exact). The accumulators
+// hold Y / 2, never a scaled-up Y, so no sum overflows where the reference's stays finite. TF32
+// rounding (ties away from zero) is "add 0x1000 to the FP32 pattern, truncate", and the truncation is
+// the round-toward-zero f16 conversion. A panel whose a' leaves f16's normal range (or whose scale
+// is subnormal) takes an FP32 path with the same products: v_mfma_f32_32x32x2_f32 on tf32(a) / 2 and
+// the TF32 features. (Halving a value below 2^-125 rounds it, an error far below the tolerance.)
 //
 // The panels are walked by a software pipeline (metadata two panels ahead, in pairs of panels at
 // F128; A values and X one panel ahead) whose memory operations are identical on every path. F128
@@ -60,7 +63,7 @@ constexpr unsigned kWave = 64;
 constexpr unsigned kSlice = 128;
 constexpr unsigned kNoPartial = 0xFFFFFFFFu;
 constexpr int kShift = 10;
-constexpr float kUnshift = 1.0f / 1024.0f;
+constexpr int kXShift = kShift + 1;
 // Buffer cache policy of the A stream (sourceIds, sourceMetadata, values): the default. The
 // nontemporal hint (2) was measured to raise L2 misses of the gathered X rows by about 1.5 GB per
 // c3 F128 launch.
@@ -94,6 +97,9 @@ constexpr std::uint64_t kBucketGroups = 0xFEDCBA9765384210ull;
 // base (offsets stay below 1 MiB); scales and X use buffers sized from `cols`, so the padding
 // sentinel source UINT32_MAX lands out of range and reads 0 without a clamp, and an absent A entry
 // reads 0 through an out-of-range offset. Wide: 64-bit global loads with clamped indices.
+// Wide with 2-byte tiles: the same, for a packed X that is u16- but not 16-byte aligned (the
+// reference's own requirement, include/format/int8_features.cuh:11-13): each 16-byte tile is read
+// as eight naturally aligned u16 loads, which never touch a byte outside the tile.
 
 struct Meta {        // one panel
     unsigned id;     // lane L: source of slot L & 7
@@ -125,11 +131,14 @@ __device__ __forceinline__ Meta pairPanel(const MetaPair& m) {
     return {pairHalf<E>(m.id), pairHalf<E>(m.mask), pairHalf<E>(m.base)};
 }
 
-template <bool Wide>
+// Addressing modes of the X and A-stream loads, chosen per launch on the host.
+enum : unsigned { kBuffer = 0, kGlobal = 1, kGlobalU16 = 2 };
+
+template <unsigned Addr>
 struct Loader;
 
 template <>
-struct Loader<false> {
+struct Loader<kBuffer> {
     static constexpr bool kWide = false;
     __amdgpu_buffer_rsrc_t ids, meta, scales, x, vals;
     unsigned first;     // task.begin: panel offsets are relative to it
@@ -179,8 +188,9 @@ struct Loader<false> {
     }
 };
 
-template <>
-struct Loader<true> {
+template <unsigned Addr>
+struct Loader {
+    static_assert(Addr == kGlobal || Addr == kGlobalU16, "64-bit addressing modes");
     static constexpr bool kWide = true;
     const KernelArgs* a;
     unsigned features;
@@ -205,8 +215,17 @@ struct Loader<true> {
         return __builtin_nontemporal_load(a->m.values + idx);
     }
     __device__ u32x4 tile(unsigned src, unsigned lane, unsigned k) const {
-        return *reinterpret_cast<const u32x4*>(a->packedX + std::size_t(min(src, a->cols - 1)) * features +
-                                               16 * (lane & 7) + kSlice * k);
+        const std::int8_t* p =
+            a->packedX + std::size_t(min(src, a->cols - 1)) * features + 16 * (lane & 7) + kSlice * k;
+        if constexpr (Addr == kGlobalU16) {
+            const unsigned short* h = reinterpret_cast<const unsigned short*>(p);
+            u32x4 t;
+#pragma unroll
+            for (unsigned i = 0; i < 4; ++i) t[i] = unsigned(h[2 * i]) | (unsigned(h[2 * i + 1]) << 16);
+            return t;
+        } else {
+            return *reinterpret_cast<const u32x4*>(p);
+        }
     }
 };
 
@@ -288,7 +307,7 @@ __device__ __forceinline__ void waveSync() {
 
 struct Lds {
     _Float16* table16; // [32 rows][8 slots] a' (f16 path)
-    float* table32;    // [32 rows][8 slots] tf32(a) * 2^kShift (FP32 path)
+    float* table32;    // [32 rows][8 slots] tf32(a) / 2 (FP32 path)
     u32x4* xtile;      // [S][8 slots][128 bytes] X rows of the panel, one block per slice
     float* mant;       // [8 slots] scale mantissas of the panel
     unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
@@ -305,9 +324,21 @@ __device__ __forceinline__ float stageTf32(const Stage& s, unsigned j) {
 // is (8g + (lane >> 3)) * 8 + k = 64g + lane. Kind G < 4 writes only row group G (the others hold
 // 0 for the whole bucket). Returns whether every entry of the panel has an exact f16 a'
 // (wave-uniform); if not, the panel contributes nothing here.
+// m * 2^-kXShift for a scale s = m * 2^e (m in [0.5, 1)): the sign and mantissa bits of s under the
+// biased exponent 126 - kXShift. One v_and_or_b32 (as cheap as a v_frexp_mant); a VOP3 takes no
+// literal and one scalar operand on gfx950, so the caller keeps the mask 0x807FFFFF in a VGPR
+// (`keep`) and the exponent bits come from an SGPR.
+__device__ __forceinline__ float shiftedMantissa(float s, unsigned keep) {
+    unsigned r;
+    asm("v_and_or_b32 %0, %1, %2, %3"
+        : "=v"(r)
+        : "v"(__float_as_uint(s)), "v"(keep), "s"(unsigned(126 - kXShift) << 23));
+    return __uint_as_float(r);
+}
+
 template <bool Wide, unsigned G, unsigned S>
 __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups, unsigned lane,
-                                                const Lds& lds, f32x16 (&acc)[4 * S]) {
+                                                const Lds& lds, f32x16 (&acc)[4 * S], unsigned keep) {
     const int e = __builtin_amdgcn_frexp_expf(s.scale);
     const bool scaleNormal = e > -126;
     bool exact = true;
@@ -330,8 +361,10 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
     const unsigned m = lane & 31, h = lane >> 5;
-    // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3.
-    lds.mant[lane & 7] = __builtin_amdgcn_frexp_mantf(s.scale);
+    // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
+    // stored as m * 2^-kXShift. For a subnormal scale the bits are not that, but such a panel's
+    // table is all zero (scaleNormal above) and the FP32 pass computes it.
+    lds.mant[lane & 7] = shiftedMantissa(s.scale, keep);
     waveSync();
     const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
     const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
@@ -358,14 +391,14 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
 }
 
 // A shared-kind panel with exact FP32 operands (v_mfma_f32_32x32x2_f32): K = 2 steps over slot
-// pairs (2j, 2j + 1), lane half h taking slot 2j + h, whose scale comes from lane 2j + h.
+// pairs (2j, 2j + 1), lane half h taking slot 2j + h, whose scale comes from lane 2j + h. The
+// products are tf32(a) / 2 * x_hat, on the accumulators' Y / 2 scale.
 template <bool Wide, unsigned S>
 __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups, unsigned lane,
                                                 const Lds& lds, f32x16 (&acc)[4 * S]) {
 #pragma unroll
     for (unsigned g = 0; g < 4; ++g)
-        lds.table32[64 * g + lane] =
-            ((groups >> g) & 1u) ? __builtin_amdgcn_ldexpf(stageTf32<Wide>(s, g), kShift) : 0.0f;
+        lds.table32[64 * g + lane] = ((groups >> g) & 1u) ? 0.5f * stageTf32<Wide>(s, g) : 0.0f;
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
     waveSync();
@@ -421,6 +454,7 @@ struct TaskWalk {
     unsigned lane;
     Lds lds;
     unsigned redoCount;      // entries in lds.redo
+    unsigned keep;           // 0x807FFFFF in a VGPR, for shiftedMantissa
 };
 
 // Queues panel `panel` for the FP32 pass when `redo` (wave-uniform) is set. The branch is taken only
@@ -475,12 +509,12 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             // is in order, so computing first would wait for loads issued only half an
             // iteration ago.
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
             ga = groupsAt(min(lo + 2 * k + 2, last));
             loadStage<G, S, Ld, false>(ld, mSecond, ga, lane, sa);
             __builtin_amdgcn_sched_barrier(0);
             sb.scale = __uint_as_float(pairHalf<0>(__float_as_uint(sc)));
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep));
             sa.scale = __uint_as_float(pairHalf<1>(__float_as_uint(sc)));
             pair = next;
             mFirst = pairPanel<0>(pair);
@@ -504,7 +538,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             g2 = groupsAt(p);
             m2 = ld.meta8(p, lane);
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
             ga = g1;
             loadStage<G, S>(ld, m1, ga, lane, sa);
             p = min(p + 1, last);
@@ -513,10 +547,10 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             g2 = groupsAt(p);
             m2 = ld.meta8(p, lane);
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep));
         }
     }
-    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc));
+    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
 }
 
 template <unsigned S, class Ld>
@@ -524,7 +558,11 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
                                          unsigned end, unsigned lane, const Lds& lds,
                                          f32x16 (&acc)[4 * S]) {
     if (begin >= end) return;
-    TaskWalk w{offsets, begin, end, lane, lds, 0u};
+    // An opaque definition keeps the mask in one VGPR for the whole walk instead of a
+    // rematerialised literal per use.
+    unsigned keep;
+    asm("v_mov_b32 %0, 0x807fffff" : "=v"(keep));
+    TaskWalk w{offsets, begin, end, lane, lds, 0u, keep};
     auto clipLo = [&](unsigned t) { return max(offsets[t], begin); };
     auto clipHi = [&](unsigned t) { return min(offsets[t], end); };
     walkPanels<0, S>(ld, w, clipLo(1), clipHi(2), acc);
@@ -532,7 +570,6 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
     walkPanels<2, S>(ld, w, clipLo(3), clipHi(4), acc);
     walkPanels<3, S>(ld, w, clipLo(4), clipHi(5), acc);
     walkPanels<kShared, S>(ld, w, clipLo(5), clipHi(16), acc);
-    // Panels whose scaled A values leave f16's normal range, again with exact FP32 operands.
     waveSync();
 #pragma unroll 1
     for (unsigned i = 0; i < w.redoCount; ++i) {
@@ -579,7 +616,7 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
 }
 
 // One task over all S = Features / 128 slices of its SW (one wave).
-template <unsigned Features, bool Wide>
+template <unsigned Features, unsigned Addr>
 __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex) {
     constexpr unsigned S = Features / kSlice;
     __shared__ __align__(16) _Float16 table16[256];
@@ -591,7 +628,7 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     const unsigned lane = threadIdx.x;
     const Sw32Task task = a.m.tasks[taskIndex];
     const unsigned sw = task.sw;
-    const Loader<Wide> ld(a, task.begin, task.end, Features);
+    const Loader<Addr> ld(a, task.begin, task.end, Features);
     const Lds lds{table16, table32, xtile, mant, redo};
 
     f32x16 acc[4 * S];
@@ -599,7 +636,7 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     for (unsigned b = 0; b < 4 * S; ++b) acc[b] = f32x16{};
     walkTask<S>(ld, a.m.bucketOffsets + std::size_t(sw) * 17, task.begin, task.end, lane, lds, acc);
 #pragma unroll
-    for (unsigned b = 0; b < 4 * S; ++b) acc[b] *= kUnshift; // exact power-of-two scaling back to Y
+    for (unsigned b = 0; b < 4 * S; ++b) acc[b] *= 2.0f; // Y / 2 to Y, exact
 
     const unsigned row = lane & 31, h = lane >> 5;
     auto sub = [&](unsigned k) -> const f32x16(&)[4] {
@@ -670,40 +707,47 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
 
 // F128: four waves per SIMD; the 64 accumulators live in ordinary VGPRs and the kernel fits 128
 // registers.
-template <bool Wide>
+template <unsigned Addr>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) void spmmInt8Kernel128(
     KernelArgs a) {
-    runTask<128, Wide>(a, xcdTask(blockIdx.x, a.m.taskCount));
+    runTask<128, Addr>(a, xcdTask(blockIdx.x, a.m.taskCount));
 }
 
 // F256: both 128-feature slices of a task in one wave (128 accumulator registers, two waves per
 // SIMD). The task's A stream, scales and A table are read and built once for both slices; measured
 // on c3 this moves 18% fewer bytes (33.1 GB against 40.5 GB) and runs 8.6% faster than one wave
 // per (task, slice).
-template <bool Wide>
+template <unsigned Addr>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 8))) void spmmInt8Kernel256(
     KernelArgs a) {
-    runTask<256, Wide>(a, xcdTask(blockIdx.x, a.m.taskCount));
+    runTask<256, Addr>(a, xcdTask(blockIdx.x, a.m.taskCount));
 }
 
 template <unsigned Features>
 void launch(const KernelArgs& args, hipStream_t stream) {
     // Buffer addressing needs the packed X and the scales within 32-bit byte offsets, with room for
-    // the padding sentinel to land out of range. TCC_SPMM_FORCE_WIDE selects the 64-bit instance
-    // for any size (used by the tests).
+    // the padding sentinel to land out of range, and 16-byte aligned X tiles. A packed X that is
+    // only u16-aligned takes the 64-bit instance with 2-byte tile loads. TCC_SPMM_FORCE_WIDE
+    // selects the 64-bit instance for any size (used by the tests).
+    const bool misaligned = reinterpret_cast<std::uintptr_t>(args.packedX) % 16 != 0;
     const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull ||
                       std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
     const dim3 grid(args.m.taskCount, 1);
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kWave), 0, stream, args); };
     if constexpr (Features == 256) {
-        if (wide)
-            hipLaunchKernelGGL((spmmInt8Kernel256<true>), grid, dim3(kWave), 0, stream, args);
+        if (misaligned)
+            go(spmmInt8Kernel256<kGlobalU16>);
+        else if (wide)
+            go(spmmInt8Kernel256<kGlobal>);
         else
-            hipLaunchKernelGGL((spmmInt8Kernel256<false>), grid, dim3(kWave), 0, stream, args);
+            go(spmmInt8Kernel256<kBuffer>);
     } else {
-        if (wide)
-            hipLaunchKernelGGL((spmmInt8Kernel128<true>), grid, dim3(kWave), 0, stream, args);
+        if (misaligned)
+            go(spmmInt8Kernel128<kGlobalU16>);
+        else if (wide)
+            go(spmmInt8Kernel128<kGlobal>);
         else
-            hipLaunchKernelGGL((spmmInt8Kernel128<false>), grid, dim3(kWave), 0, stream, args);
+            go(spmmInt8Kernel128<kBuffer>);
     }
 }
 
@@ -718,9 +762,10 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
         throw std::runtime_error("launchSpmmInt8: invalid configuration argument (no tasks)");
     if (matrix.taskCount > 0x7FFFFFFFu)
         throw std::invalid_argument("launchSpmmInt8: too many tasks for one launch");
-    // 16-byte X tiles: the packed rows must start 16-byte aligned.
-    if (reinterpret_cast<std::uintptr_t>(packedX) % 16)
-        throw std::invalid_argument("launchSpmmInt8: packedX must be 16-byte aligned");
+    // The packed features are read as u16 pairs at least (reference include/format/int8_features.cuh:
+    // 11-13 states u16 alignment); an odd address cannot be.
+    if (reinterpret_cast<std::uintptr_t>(packedX) % 2)
+        throw std::invalid_argument("launchSpmmInt8: packedX must be u16-aligned");
     const KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
                           rows,   cols};
     if (features == 128)

@@ -294,6 +294,74 @@ def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu):
     _check_windows(oracle, csr, fmt, y, pk, sc, windows, "extreme", conditioned=True)
 
 
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_huge_a_values_stay_finite(oracle, gpu, feats):
+    """A values at and above 2^118 (where tf32(a) * 2^10 would overflow FP32) up to 3e38 and 2^127,
+    one per row, with features in [-1, 1] so that every product the reference forms is finite.
+    The sources of the huge entries have zero features (q = 0: a product inf * 0 would be NaN) and
+    one of them is an all-zero row (scale 1, every q = 0). Y must be finite and match the oracle on
+    every element with the plain bound."""
+    base = T.synth_csr("t2000_20_13")
+    rng = np.random.default_rng(14)
+    off = base.row_offsets.astype(np.int64)
+    val = base.values.copy()
+    huge = np.array([2.0 ** 118, -(2.0 ** 118), 1.0e36, -1.0e36, 3.0e38, -3.0e38, 2.0 ** 127,
+                     np.nextafter(np.float32(2.0 ** 118), np.float32(0))], np.float32)
+    rows = rng.choice(base.rows, 240, replace=False)
+    picked = []
+    for i, r in enumerate(rows):
+        if off[r + 1] > off[r]:
+            e = int(rng.integers(off[r], off[r + 1]))
+            val[e] = huge[i % huge.size]
+            picked.append(e)
+    csr = T.make_canonical_csr(base.rows, base.cols, base.row_offsets, base.source_ids, val)
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = rng.uniform(-1.0, 1.0, (csr.cols, feats)).astype(np.float32)
+    huge_sources = np.unique(base.source_ids[np.array(picked)])
+    x[huge_sources, ::3] = 0.0                      # q = 0 next to the huge A values
+    x[huge_sources[0]] = 0.0                        # an all-zero row: scale 1, every q = 0
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    check_features(oracle, x, q, sc, pk)
+    assert (q[huge_sources][:, ::3] == 0).all()
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    assert np.isfinite(y).all(), f"{int((~np.isfinite(y)).sum())} non-finite outputs"
+    y_ref = oracle.sw32(csr.rows, csr.cols, *csr.views()).spmm_f64(pk, sc)
+    assert np.isfinite(y_ref).all()
+    assert np.abs(y_ref).max() > 1e37
+    assert_close(y, y_ref, f"huge A F{feats}")
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_u16_aligned_packed_x(oracle, golden, gpu, feats):
+    """packedX need only be u16-aligned, as in the reference (include/format/int8_features.cuh:11-13):
+    packed features placed 2, 6 and 14 bytes past a 16-byte boundary give Y bitwise equal to the
+    aligned launch; an odd address raises invalid_argument before any launch."""
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    for case in ("tail_33", "all_masks", "split_mixed", "random_3"):
+        rows, cols = (int(v) for v in golden[f"{case}/dims"])
+        off, src, val = (golden[f"{case}/csr_offsets"], golden[f"{case}/csr_sources"],
+                         golden[f"{case}/csr_values"])
+        fmt = T.convert_csr_to_sw32(rows, cols, T.make_canonical_csr(rows, cols, off, src, val))
+        x = features(cols, feats, seed=rows + 5 * cols, stddev=2.0)
+        packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+        _, y_aligned = _run(fmt, packed, scale, feats, gpu)
+        for shift in (2, 6, 14):
+            buf = torch.zeros(cols * feats + 32, dtype=torch.int8, device=gpu)
+            base = (16 - buf.data_ptr() % 16) % 16
+            view = buf[base + shift: base + shift + cols * feats].view(cols, feats)
+            view.copy_(packed)
+            assert view.data_ptr() % 16 == shift
+            _, y = _run(fmt, view, scale, feats, gpu)
+            assert np.array_equal(y.view(np.uint32), y_aligned.view(np.uint32)), (case, shift)
+        y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
+        assert_close(y_aligned, y_ref, f"{case} F{feats}")
+    dm = TorchDeviceMatrix(fmt, feats, device=gpu)
+    odd = torch.zeros(cols * feats + 2, dtype=torch.int8, device=gpu)[1:1 + cols * feats]
+    with pytest.raises(ValueError, match="u16-aligned"):
+        dm.spmm(odd.view(cols, feats), scale, torch.empty((rows, feats), device=gpu))
+
+
 def test_quantize_subnormal_and_huge_rows_bit_exact(oracle, gpu):
     """Subnormal features (down to a scale of a few hundred denormal quanta) and features near the
     top of the FP32 range quantize bit-exactly. Rows whose absmax / 127 underflows to zero
