@@ -33,16 +33,42 @@ def _require_cuda(*tensors) -> None:
             raise ValueError("device entry points take CUDA (HIP) tensors")
 
 
+def _require_same_device(device, *tensors) -> None:
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"tensor on {t.device}, expected {device}")
+
+
+def _require_buffer(t, name: str, dtype, min_elements: int) -> None:
+    """A kernel reads or writes `min_elements` elements of `t` from its first element: the tensor
+    must have that dtype, be contiguous and hold at least that many elements. The kernels take
+    their bounds from the sizes passed alongside (rows, cols, features), never from the allocation,
+    so a short buffer would be read or written out of bounds."""
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < min_elements:
+        raise ValueError(f"{name} holds {t.numel()} elements, needs at least {min_elements}")
+
+
 def quantize_features_int8(x: torch.Tensor, q: torch.Tensor | None = None,
                            scale: torch.Tensor | None = None, stream=None):
     """quantizeFeaturesInt8 (reference include/format/int8_features.cuh:9-10).
 
     x: float32 [sources, features] on the GPU. Returns (q int8 [sources, features], scale f32).
     """
-    _require_cuda(x)
     if x.dtype != torch.float32 or x.dim() != 2 or not x.is_contiguous():
         raise ValueError("x must be a contiguous float32 [sources, features] tensor")
     sources, features = x.shape
+    if q is not None:
+        _require_buffer(q, "q", torch.int8, sources * features)
+    if scale is not None:
+        _require_buffer(scale, "scale", torch.float32, sources)
+    _require_cuda(x, q, scale)
+    _require_same_device(x.device, q, scale)
     q = torch.empty((sources, features), dtype=torch.int8, device=x.device) if q is None else q
     scale = torch.empty(sources, dtype=torch.float32, device=x.device) if scale is None else scale
     check(lib().tcc_quantize_features_int8(_ptr(x), _ptr(q), _ptr(scale), sources, features,
@@ -52,14 +78,25 @@ def quantize_features_int8(x: torch.Tensor, q: torch.Tensor | None = None,
 
 def pack_features_int8x16(q: torch.Tensor, packed: torch.Tensor | None = None, stream=None):
     """packFeaturesInt8x16 (reference include/format/int8_features.cuh:14-15)."""
-    _require_cuda(q)
     if q.dtype != torch.int8 or q.dim() != 2 or not q.is_contiguous():
         raise ValueError("q must be a contiguous int8 [sources, features] tensor")
     sources, features = q.shape
+    if packed is not None:
+        _require_buffer(packed, "packed", torch.int8, sources * features)
+    _require_cuda(q, packed)
+    _require_same_device(q.device, packed)
     packed = torch.empty_like(q) if packed is None else packed
     check(lib().tcc_pack_features_int8x16(_ptr(q), _ptr(packed), sources, features,
                                           _stream_ptr(stream)))
     return packed
+
+
+def _check_operands(packed_x, scales, output, rows: int, cols: int, features: int) -> None:
+    _require_buffer(packed_x, "packed_x", torch.int8, cols * features)
+    _require_buffer(scales, "scales", torch.float32, cols)
+    _require_buffer(output, "output", torch.float32, rows * features)
+    _require_cuda(packed_x, scales, output)
+    _require_same_device(packed_x.device, scales, output)
 
 
 @dataclass
@@ -73,9 +110,15 @@ class SpmmWorkspace:
 def launch_spmm_int8(view: DeviceView, packed_x: torch.Tensor, scales: torch.Tensor,
                      output: torch.Tensor, rows: int, cols: int, features: int,
                      workspace: SpmmWorkspace | None = None, stream=None) -> None:
-    """launchSpmmInt8 (reference include/spmm.cuh:21-23): asynchronous on `stream`."""
-    _require_cuda(packed_x, scales, output)
+    """launchSpmmInt8 (reference include/spmm.cuh:21-23): asynchronous on `stream`.
+
+    Raises ValueError before any launch unless packed_x (int8, >= cols * features elements),
+    scales (float32, >= cols) and output (float32, >= rows * features) are contiguous tensors on
+    one GPU; the feature count itself is checked by the library (128 or 256, invalid_argument).
+    """
+    _check_operands(packed_x, scales, output, rows, cols, features)
     ws = workspace or SpmmWorkspace(None, None)
+    _require_same_device(packed_x.device, ws.partials, ws.counters)
     check(lib().tcc_launch_spmm_int8(C.byref(view), _ptr(packed_x), _ptr(scales), _ptr(output),
                                      rows, cols, features, _ptr(ws.partials), _ptr(ws.counters),
                                      _stream_ptr(stream)))
@@ -95,6 +138,9 @@ class TorchDeviceMatrix:
         arrs = fmt.arrays(copy=False)
         self.rows, self.cols = fmt.rows, fmt.cols
         self.features = features
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.tensors = {}
         for name, arr in arrs.items():
             raw = np.ascontiguousarray(arr).view(np.uint8).copy()
@@ -122,6 +168,7 @@ class TorchDeviceMatrix:
         if output is None:
             output = torch.empty((self.rows, self.features), dtype=torch.float32,
                                  device=packed_x.device)
+        _require_same_device(self.device, packed_x)
         launch_spmm_int8(self.view, packed_x, scales, output, self.rows, self.cols, self.features,
                          self.workspace(), stream)
         return output
@@ -146,6 +193,7 @@ class NativeDeviceMatrix:
 
     def spmm(self, packed_x: torch.Tensor, scales: torch.Tensor, output: torch.Tensor,
              stream=None) -> torch.Tensor:
+        _check_operands(packed_x, scales, output, self.rows, self.cols, self.features)
         check(lib().tcc_launch_spmm_int8(C.byref(self.view), _ptr(packed_x), _ptr(scales),
                                          _ptr(output), self.rows, self.cols, self.features,
                                          self.partials_ptr, self.counters_ptr,
