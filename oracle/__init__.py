@@ -9,6 +9,7 @@ Loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, never
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 import pathlib
 import subprocess
 
@@ -49,12 +50,39 @@ class _CheckStats(C.Structure):
     ]
 
 
-def _copy(ptr, count, dtype):
+def _view(ptr, count, dtype):
     dtype = np.dtype(dtype)
     if not count or not ptr:
         return np.zeros(0, dtype=dtype)
     buf = (C.c_char * (count * dtype.itemsize)).from_address(ptr)
-    return np.frombuffer(buf, dtype=dtype, count=count).copy()
+    return np.frombuffer(buf, dtype=dtype, count=count)
+
+
+def _copy(ptr, count, dtype):
+    return _view(ptr, count, dtype).copy()
+
+
+def _sha256(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8)).hexdigest()
+
+
+def csr_digests(offsets, sources, values) -> dict:
+    """SHA-256 of the three CsrMatrix arrays and the entry count."""
+    return {"row_offsets": _sha256(np.asarray(offsets, np.uint32)),
+            "source_ids": _sha256(np.asarray(sources, np.uint32)),
+            "values": _sha256(np.asarray(values, np.float32)), "nnz": int(np.asarray(sources).size)}
+
+
+def format_digests(arrays: dict, partial_count: int) -> dict:
+    """SHA-256 of every Sw32HostFormat array (bytes as laid out in memory) plus the plan's counts:
+    SWs, panels, slots, values, tasks, partial tiles (K) and split SWs (4 reductions each)."""
+    d = {name: _sha256(arrays[name]) for name in FORMAT_FIELDS}
+    d["counts"] = {"windows": int(len(arrays["window_offsets"])) - 1,
+                   "panels": int(len(arrays["row_group_masks"])),
+                   "slots": int(len(arrays["source_ids"])), "values": int(len(arrays["values"])),
+                   "tasks": int(len(arrays["tasks"])), "partial_count": int(partial_count),
+                   "split_sws": int(len(arrays["reductions"])) // 4}
+    return d
 
 
 def build() -> None:
@@ -186,18 +214,20 @@ class OracleFormat:
             self._orc.so.orc_sw32_free(C.byref(self._f))
             self._f = None
 
-    def arrays(self) -> dict:
+    def arrays(self, copy: bool = True) -> dict:
+        """The nine arrays; copy=False gives views that live as long as this object."""
         f = self._f
+        get = _copy if copy else _view
         return {
-            "window_offsets": _copy(f.windowOffsets, f.nWindowOffsets, np.uint32),
-            "source_ids": _copy(f.sourceIds, f.nSlots, np.uint32),
-            "row_group_masks": _copy(f.rowGroupMasks, f.nPanels, np.uint32),
-            "source_metadata": _copy(f.sourceMetadata, f.nSlots, np.uint64),
-            "values": _copy(f.values, f.nValues, np.float32),
-            "bucket_offsets": _copy(f.bucketOffsets, f.nBucketOffsets, np.uint32),
-            "tasks": _copy(f.tasks, f.nTasks, TASK_DTYPE),
-            "reductions": _copy(f.reductions, f.nReductions, REDUCE_DTYPE),
-            "partial_ids": _copy(f.partialIds, f.nPartialIds, np.uint32),
+            "window_offsets": get(f.windowOffsets, f.nWindowOffsets, np.uint32),
+            "source_ids": get(f.sourceIds, f.nSlots, np.uint32),
+            "row_group_masks": get(f.rowGroupMasks, f.nPanels, np.uint32),
+            "source_metadata": get(f.sourceMetadata, f.nSlots, np.uint64),
+            "values": get(f.values, f.nValues, np.float32),
+            "bucket_offsets": get(f.bucketOffsets, f.nBucketOffsets, np.uint32),
+            "tasks": get(f.tasks, f.nTasks, TASK_DTYPE),
+            "reductions": get(f.reductions, f.nReductions, REDUCE_DTYPE),
+            "partial_ids": get(f.partialIds, f.nPartialIds, np.uint32),
         }
 
     def spmm_f64(self, packed, scales) -> np.ndarray:
@@ -328,7 +358,9 @@ class RefFormat:
             raise OracleError(st)
         return self._csr_out(h)
 
-    def convert(self, rows, cols, offsets, sources, values, bucket=True) -> dict:
+    def convert(self, rows, cols, offsets, sources, values, bucket=True, digests=False) -> dict:
+        """The reference's convertCsrToSw32 output: the nine arrays and partial_count, or with
+        digests=True only format_digests() of them (no copies, for configuration-size inputs)."""
         off = np.ascontiguousarray(offsets, np.uint32)
         src = np.ascontiguousarray(sources, np.uint32)
         val = np.ascontiguousarray(values, np.float32)
@@ -338,10 +370,13 @@ class RefFormat:
         if st:
             raise OracleError(st)
         out = {}
+        get = _view if digests else _copy
         for idx, name, dt in self.ARRAYS:
             p = C.c_void_p()
             nbytes = self.so.ref_array(h, idx, C.byref(p))
-            out[name] = _copy(p.value, nbytes // np.dtype(dt).itemsize, dt)
+            out[name] = get(p.value, nbytes // np.dtype(dt).itemsize, dt)
         out["partial_count"] = int(self.so.ref_partial_count(h))
+        if digests:
+            out = format_digests(out, out["partial_count"])
         self.so.ref_free(h)
         return out

@@ -5,10 +5,16 @@ reference's makeCanonicalCsr / convertCsrToSw32 (with its internal buildPanelTas
 loadMatrixMarket, compiled from /root/reference/src/format/*.cpp into oracle/_ref/libref_format.so
 by oracle/Makefile. Only data is committed: inputs and the reference's outputs.
 
+It also writes tests/golden/config_digests.json: SHA-256 digests and counts of the reference's
+convertCsrToSw32 output (all nine arrays, partialCount) for the synthetic configurations c1, c2, c3
+and c5 (c4 shares c3's matrix), and of its makeCanonicalCsr output for a non-canonical input of c2's
+size (noncanonical_from below). The matrices come from this repository's deterministic generator.
+
 Run from the repository root:  python tests/golden/make_fixtures.py
 """
 from __future__ import annotations
 
+import json
 import pathlib
 import sys
 import tempfile
@@ -18,7 +24,7 @@ import numpy as np
 ROOT = pathlib.Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
-from oracle import OracleError, RefFormat, build  # noqa: E402
+from oracle import OracleError, RefFormat, build, csr_digests  # noqa: E402
 
 OUT = pathlib.Path(__file__).resolve().parent
 FIELDS = ("window_offsets", "source_ids", "row_group_masks", "source_metadata", "values",
@@ -145,6 +151,56 @@ def mtx_cases():
     }
 
 
+DIGEST_CONFIGS = ("c1", "c2", "c5", "c3")
+
+
+def noncanonical_from(offsets, sources, values, seed):
+    """A raw CSR with the same row sums as (offsets, sources, values) that exercises every rule of
+    canonicalisation at scale: entries of each row in random order, one entry in ten split into two
+    halves (duplicates to coalesce in input order) and one in fifty joined by a +w / -w pair on a
+    random column (zero sums to drop, or extra terms on an existing column)."""
+    rng = np.random.default_rng(seed)
+    off = np.asarray(offsets, np.int64)
+    src = np.asarray(sources, np.uint32)
+    val = np.asarray(values, np.float32)
+    rows = np.repeat(np.arange(off.size - 1, dtype=np.int64), np.diff(off))
+    cols = int(src.max()) + 1 if src.size else 1
+    half = rng.random(src.size) < 0.1
+    val = val.copy()
+    val[half] *= np.float32(0.5)
+    pair = np.flatnonzero(rng.random(src.size) < 0.02)
+    pcol = rng.integers(0, cols, pair.size).astype(np.uint32)
+    pw = rng.uniform(-1, 1, pair.size).astype(np.float32)
+    all_rows = np.concatenate([rows, rows[half], rows[pair], rows[pair]])
+    all_src = np.concatenate([src, src[half], pcol, pcol])
+    all_val = np.concatenate([val, val[half], pw, -pw])
+    order = np.lexsort((rng.random(all_rows.size), all_rows))
+    new_off = np.concatenate([[0], np.cumsum(np.bincount(all_rows, minlength=off.size - 1))])
+    return new_off.astype(np.uint32), all_src[order], all_val[order]
+
+
+def config_digests(ref):
+    """Digests of the reference's format for each configuration and of its canonical CSR of a
+    non-canonical c2-sized input."""
+    import tcc_spmm_amd as T
+    out = {"configs": {}, "canonical": {}}
+    for cfg in DIGEST_CONFIGS:
+        csr = T.synth_csr(cfg)
+        off, src, val = csr.views()
+        out["configs"][cfg] = {"dims": [csr.rows, csr.cols], "csr": csr_digests(off, src, val),
+                               "format": ref.convert(csr.rows, csr.cols, off, src, val, True,
+                                                     digests=True)}
+        print(f"{cfg}: {out['configs'][cfg]['format']['counts']}", flush=True)
+        if cfg == "c2":
+            raw = noncanonical_from(off, src, val, seed=2026)
+            canon = ref.canonical_csr(csr.rows, csr.cols, *raw)
+            out["canonical"]["c2_noncanonical"] = {
+                "dims": [csr.rows, csr.cols], "seed": 2026, "raw": csr_digests(*raw),
+                "canonical": csr_digests(*canon)}
+        del csr
+    return out
+
+
 def main():
     build()
     if not RefFormat.available():
@@ -226,6 +282,9 @@ def main():
     np.savez_compressed(OUT / "format_reference.npz", **store)
     print(f"wrote {OUT / 'format_reference.npz'}: {len(names)} format cases, {len(errs)} + "
           f"{len(conv_errs)} error cases, {len(mtx)} Matrix Market cases")
+    digests = config_digests(ref)
+    (OUT / "config_digests.json").write_text(json.dumps(digests, indent=1, sort_keys=True) + "\n")
+    print(f"wrote {OUT / 'config_digests.json'}: {', '.join(digests['configs'])}")
 
 
 if __name__ == "__main__":
