@@ -160,15 +160,25 @@ void buildPanelTasks(Sw32HostFormat& format) {
     format.partialCount = fit32(tiles);
 }
 
+namespace {
+// The CSR must describe `rows` x `cols`: rows + 1 offsets running from 0 to the entry count without
+// decreasing, one value per source id. (The exception messages are the reference's, part of the
+// observable behaviour.) Entry-level rules are checked per SW while the stream is built.
+void requireCsrLayout(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr) {
+    const std::vector<std::uint32_t>& off = csr.rowOffsets;
+    const std::size_t entries = csr.sourceIds.size();
+    const bool sized = rows != 0 && cols != 0 && off.size() == std::size_t(rows) + 1 &&
+                       csr.values.size() == entries;
+    if (!sized || off.front() != 0 || off.back() != entries)
+        throw std::invalid_argument("invalid canonical CSR for source-mask SW32");
+    if (!std::is_sorted(off.begin(), off.end()))
+        throw std::invalid_argument("decreasing CSR offsets");
+}
+} // namespace
+
 Sw32HostFormat convertCsrToSw32(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr,
                                 bool bucketByRwMask) {
-    if (!rows || !cols || csr.rowOffsets.size() != std::size_t(rows) + 1 ||
-        csr.rowOffsets.front() != 0 || csr.rowOffsets.back() != csr.sourceIds.size() ||
-        csr.values.size() != csr.sourceIds.size())
-        throw std::invalid_argument("invalid canonical CSR for source-mask SW32");
-    for (std::uint32_t r = 0; r < rows; ++r)
-        if (csr.rowOffsets[r] > csr.rowOffsets[r + 1])
-            throw std::invalid_argument("decreasing CSR offsets");
+    requireCsrLayout(rows, cols, csr);
 
     const std::uint32_t windows = std::uint32_t((std::uint64_t(rows) + 31) / 32);
     // Blocks of consecutive SWs balanced by entry count, so power-law rows do not serialise.

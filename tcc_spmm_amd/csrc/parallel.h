@@ -21,20 +21,32 @@ inline unsigned hostThreads() {
 }
 
 // Run body(chunkIndex, begin, end) over [0, n) split into `chunks` contiguous ranges, on up to
-// hostThreads() threads. The first exception thrown by any chunk is rethrown after all finish.
+// hostThreads() threads. If chunks throw, the exception of the lowest-indexed failing chunk is
+// rethrown after all threads finish, so the error reported is the first in range order whatever the
+// timing (a chunk that walks its range in order reports its first defect). Chunks after a failed
+// one are skipped once the failure is known.
 template <typename Body>
 void parallelChunks(std::size_t n, std::size_t chunks, Body body) {
     if (chunks == 0) return;
     const unsigned workers = unsigned(std::min<std::size_t>(hostThreads(), chunks));
     std::exception_ptr error;
+    std::size_t errorChunk = chunks; // lowest failing chunk so far
     std::mutex errorLock;
+    auto failedBefore = [&](std::size_t c) {
+        std::lock_guard<std::mutex> g(errorLock);
+        return errorChunk < c;
+    };
     auto run = [&](unsigned w) {
         for (std::size_t c = w; c < chunks; c += workers) {
+            if (failedBefore(c)) break;
             try {
                 body(c, n * c / chunks, n * (c + 1) / chunks);
             } catch (...) {
                 std::lock_guard<std::mutex> g(errorLock);
-                if (!error) error = std::current_exception();
+                if (c < errorChunk) {
+                    errorChunk = c;
+                    error = std::current_exception();
+                }
             }
         }
     };

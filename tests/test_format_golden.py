@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import tcc_spmm_amd as T
+from oracle import OracleError
 
 FIELDS = ("window_offsets", "source_ids", "row_group_masks", "source_metadata", "values",
           "bucket_offsets", "tasks", "reductions", "partial_ids")
@@ -145,3 +146,51 @@ def test_matrix_market_matches_reference(golden, tmp_path):
         assert _same_bytes(csr.row_offsets, golden[f"{name}/csr_offsets"]), name
         assert _same_bytes(csr.source_ids, golden[f"{name}/csr_sources"]), name
         assert _same_bytes(csr.values, golden[f"{name}/csr_values"]), name
+
+
+def _rows_csr(rows, per_row, cols, rng):
+    src = np.concatenate([np.sort(rng.choice(cols, per_row, replace=False)) for _ in range(rows)])
+    off = np.arange(0, rows * per_row + 1, per_row, dtype=np.uint32)
+    return off, src.astype(np.uint32), rng.uniform(0.5, 1.0, src.size).astype(np.float32)
+
+
+@pytest.mark.parametrize("first,second", [("overflow", "column"), ("column", "overflow"),
+                                          ("nan", "overflow")])
+def test_canonical_csr_reports_first_defect_in_row_order(ref_format, first, second):
+    """Two defects in rows thousands apart (different parallel blocks): the message is the first
+    row's, as in the reference's row-by-row scan (src/format/csr.cpp:15-36)."""
+    rows, cols, per = 6000, 500, 6
+    off, src, val = _rows_csr(rows, per, cols, np.random.default_rng(8))
+    for row, kind in ((150, first), (4700, second)):
+        e = row * per
+        if kind == "overflow":      # a duplicate pair whose FP32 sum overflows
+            src[e + 1] = src[e]
+            val[e:e + 2] = np.float32(3e38)
+        elif kind == "column":
+            src[e + 2] = cols
+        else:
+            val[e + 3] = np.nan
+    with pytest.raises(OracleError) as ref:
+        ref_format.canonical_csr(rows, cols, off, src, val)
+    with pytest.raises(ValueError) as got:
+        T.make_canonical_csr(rows, cols, off, src, val)
+    want = {"overflow": "nonfinite coalesced weight",
+            "column": "invalid CSR column or nonfinite value",
+            "nan": "invalid CSR column or nonfinite value"}[first]
+    assert want in str(got.value)
+    assert ref.value.code == 1  # invalid_argument
+
+
+def test_conversion_reports_first_defective_sw(ref_format):
+    """A zero value in SW 3 and a repeated source in SW 150 (different SW blocks of the parallel
+    builder): the reported message is SW 3's."""
+    rows, cols, per = 6400, 700, 5
+    off, src, val = _rows_csr(rows, per, cols, np.random.default_rng(9))
+    val[3 * 32 * per + 7] = 0.0
+    e = 150 * 32 * per + 11
+    src[e + 1] = src[e]
+    raw = T.csr_from_arrays(rows, cols, off, src, val)
+    with pytest.raises(ValueError, match="finite nonzero"):
+        T.convert_csr_to_sw32(rows, cols, raw)
+    with pytest.raises(OracleError):
+        ref_format.convert(rows, cols, off, src, val)
