@@ -4,6 +4,8 @@
 #pragma once
 #include "format/sw32.h"
 
+#include <cstddef>
+
 #include <hip/hip_runtime_api.h>
 
 // Scratch the caller owns for one launch at a time; launches queued one after another on a single
@@ -31,3 +33,22 @@ struct SpmmWorkspace {
 void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
                     float* output, std::uint32_t rows, std::uint32_t cols, std::uint32_t features,
                     SpmmWorkspace workspace, hipStream_t stream = nullptr);
+
+// Bytes of the library-owned scratch behind launchSpmmInt8NoAlloc, per GPU: room for the split-SW
+// workspace of c3 at F=128 (14,731 partial tiles, 60.6 MB).
+constexpr std::size_t kNoAllocScratchBytes = std::size_t(64) << 20;
+
+// launchSpmmInt8 without a caller workspace: no counterpart in the reference. For callers that
+// cannot allocate device memory (HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc): the completion counters and partial tiles live in a static device array of
+// kNoAllocScratchBytes that each GPU holds until the process ends, and the call itself allocates
+// nothing. partialCount is Sw32HostFormat::partialCount of the uploaded plan (the workspace size
+// derives from it); a plan whose counters and partial tiles exceed the scratch throws
+// std::invalid_argument before any launch, as do feature counts other than 128 or 256. Every call
+// on one GPU shares that GPU's scratch: calls that can overlap on one GPU (other streams, or
+// concurrent host threads) race and must be serialised by the caller. Other behaviour is
+// launchSpmmInt8's.
+void launchSpmmInt8NoAlloc(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
+                           float* output, std::uint32_t rows, std::uint32_t cols,
+                           std::uint32_t features, std::uint32_t partialCount,
+                           hipStream_t stream = nullptr);

@@ -94,6 +94,14 @@ void tcc_sw32_free(tcc_sw32* format);
 int tcc_launch_spmm_int8(const tcc_device_view* matrix, const int8_t* packedX, const float* scales,
                          float* output, uint32_t rows, uint32_t cols, uint32_t features,
                          float* partials, uint32_t* counters, void* stream);
+/* launchSpmmInt8NoAlloc (include/spmm.h) — no counterpart in the reference. For callers that cannot
+ * allocate (HIP graph capture, serving loops): the split-SW workspace lives in a library-owned
+ * static device array of kNoAllocScratchBytes (64 MiB) per GPU, and the call allocates nothing.
+ * partialCount is the plan's Sw32HostFormat::partialCount; a plan whose workspace does not fit
+ * returns TCC_INVALID_ARGUMENT before any launch. Calls that overlap on one GPU race. */
+int tcc_launch_spmm_int8_noalloc(const tcc_device_view* matrix, const int8_t* packedX,
+                                 const float* scales, float* output, uint32_t rows, uint32_t cols,
+                                 uint32_t features, uint32_t partialCount, void* stream);
 /* quantizeFeaturesInt8 — reference include/format/int8_features.cuh:9-10. */
 int tcc_quantize_features_int8(const float* x, int8_t* q, float* scale, uint32_t sources,
                                uint32_t features, void* stream);

@@ -184,6 +184,16 @@ int tcc_launch_spmm_int8(const tcc_device_view* matrix, const int8_t* packedX, c
     });
 }
 
+int tcc_launch_spmm_int8_noalloc(const tcc_device_view* matrix, const int8_t* packedX,
+                                 const float* scales, float* output, uint32_t rows, uint32_t cols,
+                                 uint32_t features, uint32_t partialCount, void* stream) {
+    return guarded([&] {
+        if (!matrix) throw std::invalid_argument("null device view");
+        launchSpmmInt8NoAlloc(toView(matrix), packedX, scales, output, rows, cols, features,
+                              partialCount, static_cast<hipStream_t>(stream));
+    });
+}
+
 int tcc_quantize_features_int8(const float* x, int8_t* q, float* scale, uint32_t sources,
                                uint32_t features, void* stream) {
     return guarded([&] {

@@ -45,10 +45,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 #include <stdexcept>
+#include <string>
 #include <type_traits>
 
 namespace {
@@ -773,4 +776,71 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
     else
         launch<256>(args, stream);
     checkHip(hipGetLastError());
+}
+
+// ------------------------------------------------------------------------------------------------
+// Allocation-free entry point (no counterpart in the reference): the split-SW workspace lives in a
+// library-owned device array instead of caller buffers. Layout: completion counters
+// [ceil(rows/32)][F/128] from offset 0, then the partial tiles [K][8][F] from the next 256-byte
+// boundary. Every GPU the library runs on holds its own copy for the life of the process.
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratchLock;
+void* scratchAddress[kMaxDevices]; // device address of `scratch` per device, found once
+
+// The address of the current device's `scratch`. In host code the array's name is only a stand-in
+// for the symbol, never a device pointer, so the address is looked up once per device (with that
+// device current) and reused.
+void* deviceScratch() {
+    int device = 0;
+    checkHip(hipGetDevice(&device));
+    if (device < 0 || device >= kMaxDevices)
+        throw std::runtime_error("launchSpmmInt8NoAlloc: device index out of range");
+    std::lock_guard<std::mutex> guard(scratchLock);
+    if (!scratchAddress[device]) {
+        void* address = nullptr;
+        checkHip(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
+        scratchAddress[device] = address;
+    }
+    return scratchAddress[device];
+}
+
+// Zero `count` words: a kernel rather than hipMemsetAsync, so the entry point can be captured into
+// a HIP graph.
+__global__ __launch_bounds__(256) void clearWords(unsigned* words, unsigned count) {
+    for (unsigned i = blockIdx.x * 256 + threadIdx.x; i < count; i += gridDim.x * 256) words[i] = 0;
+}
+
+} // namespace
+
+void launchSpmmInt8NoAlloc(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
+                           float* output, std::uint32_t rows, std::uint32_t cols,
+                           std::uint32_t features, std::uint32_t partialCount, hipStream_t stream) {
+    if (features != 128 && features != 256)
+        throw std::invalid_argument("feature dimension must be 128 or 256");
+    SpmmWorkspace workspace;
+    if (partialCount) {
+        const std::uint64_t counters = (std::uint64_t(rows) + 31) / 32 * (features / 128);
+        const std::uint64_t counterBytes = (counters * 4 + 255) / 256 * 256;
+        const std::uint64_t partialBytes = std::uint64_t(partialCount) * 8 * features * 4;
+        if (counterBytes + partialBytes > kNoAllocScratchBytes)
+            throw std::invalid_argument(
+                "launchSpmmInt8NoAlloc: the plan's " + std::to_string(partialCount) +
+                " partial tiles at F=" + std::to_string(features) + " need " +
+                std::to_string(counterBytes + partialBytes) + " bytes of scratch, more than its " +
+                std::to_string(kNoAllocScratchBytes) + "; use launchSpmmInt8 with a workspace");
+        unsigned char* base = static_cast<unsigned char*>(deviceScratch());
+        workspace.counters = reinterpret_cast<std::uint32_t*>(base);
+        workspace.partials = reinterpret_cast<float*>(base + counterBytes);
+        // The counters must start at zero; a previous call leaves them at zero unless it failed.
+        const unsigned blocks = unsigned(std::min<std::uint64_t>((counters + 255) / 256, 1024));
+        hipLaunchKernelGGL(clearWords, dim3(blocks), dim3(256), 0, stream, workspace.counters,
+                           unsigned(counters));
+        checkHip(hipGetLastError());
+    }
+    launchSpmmInt8(matrix, packedX, scales, output, rows, cols, features, workspace, stream);
 }

@@ -124,6 +124,18 @@ def launch_spmm_int8(view: DeviceView, packed_x: torch.Tensor, scales: torch.Ten
                                      _stream_ptr(stream)))
 
 
+def launch_spmm_int8_noalloc(view: DeviceView, packed_x: torch.Tensor, scales: torch.Tensor,
+                             output: torch.Tensor, rows: int, cols: int, features: int,
+                             partial_count: int, stream=None) -> None:
+    """launchSpmmInt8NoAlloc (include/spmm.h; no counterpart in the reference): launchSpmmInt8
+    with the split-SW workspace in the library's own per-GPU scratch, allocating nothing.
+    partial_count is the plan's Sw32HostFormat.partial_count. Calls that overlap on one GPU race."""
+    _check_operands(packed_x, scales, output, rows, cols, features)
+    check(lib().tcc_launch_spmm_int8_noalloc(C.byref(view), _ptr(packed_x), _ptr(scales),
+                                             _ptr(output), rows, cols, features, partial_count,
+                                             _stream_ptr(stream)))
+
+
 class TorchDeviceMatrix:
     """Uploads every array of a bucketed Sw32HostFormat into torch tensors and builds the view.
 

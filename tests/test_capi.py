@@ -93,3 +93,25 @@ def test_header_structs_match_cpp_layouts():
     assert ctypes.sizeof(DeviceView) == 10 * 8  # 9 pointers + uint32 padded to 8
     header = (ROOT / "include" / "format" / "sw32.h").read_text()
     assert "static_assert(sizeof(Sw32Task) == 28" in header
+
+
+def test_noalloc_entry_point_rejects_before_any_launch():
+    """launchSpmmInt8NoAlloc checks the feature count and the size of the plan's workspace against
+    its fixed scratch before touching the GPU, so both rejections run on a CPU-only host."""
+    from tcc_spmm_amd._lib import DeviceView, lib
+    view = DeviceView()
+    view.taskCount = 1
+    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 32, 32, 64, 1,
+                                            None)
+    assert st == 1 and b"128 or 256" in lib().tcc_last_error()
+    # c3 at F=256: 14,731 partial tiles of 8 KiB need 120.7 MB, more than the 64 MiB scratch.
+    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 2449029,
+                                            2449029, 256, 14731, None)
+    assert st == 1 and b"scratch" in lib().tcc_last_error()
+    # The largest plan that fits at F=128 for 4096 rows: 128 counters (one 256-byte block) plus
+    # K tiles of 4 KiB in 64 MiB.
+    k_max = ((64 << 20) - 256) // (8 * 128 * 4)
+    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 4096, 4096, 128,
+                                            k_max + 1, None)
+    assert st == 1 and b"scratch" in lib().tcc_last_error()
+    assert b"noalloc" in (ROOT / "include" / "tcc_spmm_c.h").read_bytes()
