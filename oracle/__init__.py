@@ -10,13 +10,15 @@ from __future__ import annotations
 
 import ctypes as C
 import hashlib
+import os
 import pathlib
 import subprocess
 
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-ORACLE_SO = HERE / "_build" / "liboracle.so"
+# TCC_ORACLE_LIB selects another build of the checker (the sanitizer build: make -C oracle san).
+ORACLE_SO = pathlib.Path(os.environ.get("TCC_ORACLE_LIB") or HERE / "_build" / "liboracle.so")
 REF_SO = HERE / "_ref" / "libref_format.so"
 
 TASK_DTYPE = np.dtype([(n, "<u4") for n in ("sw", "begin", "end", "partial", "mask", "chunks",

@@ -285,7 +285,7 @@ int orc_sw32_convert(uint32_t rows, uint32_t cols, const uint32_t* rowOffsets,
                 ++n;
             }
         }
-        qsort(trip, n, sizeof(triple_t), triple_cmp); /* ascending (source, row): the merge order */
+        if (n) qsort(trip, n, sizeof(triple_t), triple_cmp); /* ascending (source, row): the merge order */
         for (int i = 0; i < 16; ++i) buckets[i].n = 0;
         size_t nv = 0;
         for (size_t i = 0; i < n;) { /* :102-129 */

@@ -6,9 +6,12 @@ if it is missing, every entry point raises instead of falling back to anything e
 from __future__ import annotations
 
 import ctypes as C
+import os
 import pathlib
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtcc_spmm.so"
+# TCC_SPMM_LIB selects another build of the library (the sanitizer build of tcc_spmm_amd.build).
+LIB_PATH = pathlib.Path(os.environ.get("TCC_SPMM_LIB") or
+                        pathlib.Path(__file__).resolve().parent / "libtcc_spmm.so")
 
 u32p = C.POINTER(C.c_uint32)
 u64p = C.POINTER(C.c_uint64)

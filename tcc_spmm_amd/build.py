@@ -109,7 +109,58 @@ def build_oracle(verbose: bool = False) -> None:
         print("built oracle")
 
 
+SAN_DIR = PKG / "_san"
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+             "-fno-sanitize-recover=undefined"]
+
+
+def build_sanitized(verbose: bool = False) -> pathlib.Path:
+    """AddressSanitizer + UBSan build of the host code, for CPU test runs only.
+
+    The host C++ sources (format builders, Matrix Market reader, C ABI, synthetic generators) are
+    compiled by clang with the sanitizers; the HIP sources keep their ordinary build, since the
+    sanitizers here cover host code only. The result goes to tcc_spmm_amd/_san/libtcc_spmm.so and
+    oracle/_san/liboracle.so; run the CPU suite against them with clang's ASan runtime preloaded:
+
+        python -m tcc_spmm_amd.build --sanitize
+        TCC_SPMM_LIB=tcc_spmm_amd/_san/libtcc_spmm.so TCC_ORACLE_LIB=oracle/_san/liboracle.so \
+        LD_PRELOAD=$(/opt/rocm/llvm/bin/clang -print-file-name=libclang_rt.asan-x86_64.so) \
+        ASAN_OPTIONS=detect_leaks=0 python -m pytest tests -m "not gpu"
+    """
+    SAN_DIR.mkdir(exist_ok=True)
+    build()  # the ordinary objects, HIP ones included
+    clang = str(ROCM / "llvm" / "bin" / "clang++")
+    objs = []
+    for src in _sources():
+        if src.suffix == ".hip":
+            objs.append(BUILD / (str(src.relative_to(CSRC)).replace(os.sep, "__") + ".o"))
+            continue
+        obj = SAN_DIR / (str(src.relative_to(CSRC)).replace(os.sep, "__") + ".o")
+        cmd = [clang, *SAN_FLAGS, *[f for f in CXX_FLAGS if f != "-O3"], "-c", str(src), "-o",
+               str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"compile failed: {shlex.join(cmd)}\n{res.stderr}")
+        objs.append(obj)
+    out = SAN_DIR / "libtcc_spmm.so"
+    cmd = [str(ROCM / "bin" / "hipcc"), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(out),
+           *map(str, objs), "-lpthread"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {shlex.join(cmd)}\n{res.stderr}")
+    res = subprocess.run(["make", "-s", "-C", str(ROOT / "oracle"), "san"], capture_output=True,
+                         text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle sanitizer build failed:\n{res.stdout}\n{res.stderr}")
+    if verbose:
+        print(f"built {out} and oracle/_san/liboracle.so")
+    return out
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--sanitize" in sys.argv:
+        build_sanitized(verbose=True)
+    else:
+        build(verbose=True)
     if "--with-oracle" in sys.argv:
         build_oracle(verbose=True)

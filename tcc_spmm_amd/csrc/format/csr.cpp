@@ -15,7 +15,6 @@
 
 #include <algorithm>
 #include <cmath>
-#include <cstring>
 #include <stdexcept>
 
 namespace {
@@ -101,8 +100,8 @@ CsrMatrix makeCanonicalCsr(std::uint32_t rows, std::uint32_t cols, std::uint32_t
         for (std::size_t r = r0; r < r1; ++r) {
             const std::uint32_t from = rowOffsets[r], to = out.rowOffsets[r], n = keptPerRow[r];
             if (!n) continue;
-            std::memcpy(out.sourceIds.data() + to, stageCols.data() + from, n * sizeof(std::uint32_t));
-            std::memcpy(out.values.data() + to, stageVals.data() + from, n * sizeof(float));
+            std::copy_n(stageCols.begin() + from, n, out.sourceIds.begin() + to);
+            std::copy_n(stageVals.begin() + from, n, out.values.begin() + to);
         }
     });
     return out;

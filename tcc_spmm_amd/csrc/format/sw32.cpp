@@ -224,16 +224,16 @@ Sw32HostFormat convertCsrToSw32(std::uint32_t rows, std::uint32_t cols, const Cs
         const WindowBlock& p = parts[b];
         const std::uint32_t panel0 = std::uint32_t(panelAt[b]);
         const std::uint64_t value0 = valueAt[b];
-        std::memcpy(out.sourceIds.data() + slotAt[b], p.sourceIds.data(), p.sourceIds.size() * 4);
+        std::copy_n(p.sourceIds.begin(), p.sourceIds.size(), out.sourceIds.begin() + slotAt[b]);
         for (std::size_t i = 0; i < p.metadata.size(); ++i) {
             const std::uint64_t m = p.metadata[i];
             // Padding slots keep metadata 0; real slots get the global value base.
             out.sourceMetadata[slotAt[b] + i] =
                 p.sourceIds[i] == kPad ? m : m + (value0 << 32);
         }
-        std::memcpy(out.rowGroupMasks.data() + panelAt[b], p.rowGroupMasks.data(),
-                    p.rowGroupMasks.size() * 4);
-        std::memcpy(out.values.data() + value0, p.values.data(), p.values.size() * 4);
+        std::copy_n(p.rowGroupMasks.begin(), p.rowGroupMasks.size(),
+                    out.rowGroupMasks.begin() + panelAt[b]);
+        std::copy_n(p.values.begin(), p.values.size(), out.values.begin() + value0);
         for (std::size_t i = 0; i < p.windowEnds.size(); ++i)
             out.windowOffsets[cut[b] + 1 + i] = p.windowEnds[i] + panel0;
         for (std::size_t i = 0; i < p.bucketOffsets.size(); ++i)

@@ -112,8 +112,8 @@ void fillRows(Csr& a, std::uint64_t seed, const std::vector<std::uint32_t>& degr
                                 distinctColumns(g, a.cols, degree[r],
                                                 [&](Rng& gg) { return draw(gg, std::uint32_t(r)); },
                                                 cols);
-                                std::memcpy(a.columns.data() + a.offsets[r], cols.data(),
-                                            cols.size() * 4);
+                                std::copy(cols.begin(), cols.end(),
+                                          a.columns.begin() + a.offsets[r]);
                             }
                         });
     tcc::parallelChunks(a.rows, std::min<std::size_t>(a.rows, 2048),
