@@ -17,9 +17,9 @@ request counters give the same read bytes within 0.2%) is read from
 profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present;
 `traffic_bw` is that traffic over the measured time (the memory system's actual load).
 
-cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c), median of 5 runs over a
-bounded prefix of SWs (~10 s of CPU work in total), scaled by panel share to one full SpMM; plus a
-single-thread figure over a smaller prefix (~5 s).
+cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over the whole workload, median
+of 5 runs on up to 16 threads (about 10 s of CPU work); plus a single-thread figure over a prefix of SWs
+(~5 s), scaled by panel share.
 """
 from __future__ import annotations
 
@@ -131,13 +131,14 @@ def run_workload(csr, fmt, features, seed, steps, warmup, dev):
     return ms, means, y0, prep
 
 
-def cpu_baseline(csr, fmt, features, seed, budget_s=10.0, single_budget_s=5.0):
+def cpu_baseline(csr, fmt, features, seed, single_budget_s=5.0):
     """Oracle FP32 SpMM on the host (dequantization, TF32 operands, FP32 row-order accumulation).
 
-    Multithreaded (up to 16 threads, the GPU box's CPU share): one warm-up over a probe prefix of
-    SWs, then 5 timed runs over a prefix sized for about `budget_s` of work in total; the median,
-    scaled by the prefix's share of panels, is one full SpMM. Single-threaded: one run over a prefix
-    sized for about `single_budget_s`, scaled the same way.
+    Multithreaded, over the whole workload: one warm-up over a prefix of SWs, then 5 runs over all
+    SWs; the median is the figure. Threads: the host's cores up to 16, the CPU share of a one-GPU
+    box (its worker pools are capped there). Single-threaded: one run over a prefix sized for about
+    `single_budget_s`, scaled by the prefix's share of panels (a full single-thread run would take
+    about half a minute).
     """
     import tcc_spmm_amd as T
     from oracle import Oracle
@@ -163,19 +164,18 @@ def cpu_baseline(csr, fmt, features, seed, budget_s=10.0, single_budget_s=5.0):
         return time.time() - t, used
 
     probe = min(n_sw, 2000)
-    dt, _ = timed(probe, threads)  # warm-up
-    sample = min(n_sw, max(probe, int(probe * budget_s / 5 / max(dt, 1e-3))))
-    runs = [timed(sample, threads) for _ in range(5)]
+    timed(probe, threads)  # warm-up
+    runs = [timed(n_sw, threads) for _ in range(5)]
     used = runs[0][1]
-    ms_full = float(np.median([r[0] for r in runs])) * 1e3 / share(sample)
+    ms_full = float(np.median([r[0] for r in runs])) * 1e3
     dt1, _ = timed(probe // 4, 1)
     sample1 = min(n_sw, max(probe // 4, int(probe // 4 * single_budget_s / max(dt1, 1e-3))))
     dt1, _ = timed(sample1, 1)
     ms_single = dt1 * 1e3 / share(sample1)
     return {"value": round(ms_full, 3), "unit": "ms/SpMM", "cores": int(used), "kind": "port",
-            "sample": f"median of 5 runs over the first {sample} of {n_sw} SWs ({share(sample):.1%} of "
-                      f"panels), FP32 TF32-operand SpMM from oracle/tcc_oracle.c with {used} threads, "
-                      f"scaled by panel share",
+            "sample": f"the whole workload ({n_sw} SWs, all panels), median of 5 runs after a "
+                      f"warm-up; FP32 TF32-operand SpMM from oracle/tcc_oracle.c with {used} threads",
+            "runs_ms": [round(r[0] * 1e3, 1) for r in runs],
             "single_thread": {"value": round(ms_single, 1), "unit": "ms/SpMM", "cores": 1,
                               "sample": f"first {sample1} SWs ({share(sample1):.1%} of panels), "
                                         f"{dt1:.1f}s measured, scaled by panel share"}}
