@@ -17,6 +17,13 @@ request counters give the same read bytes within 0.2%) is read from
 profiles/spmmInt8Kernel_<workload>_f<F>_counters.json when a counter profile of this workload is present;
 `traffic_bw` is that traffic over the measured time (the memory system's actual load).
 
+Traffic floor (model/, an L2 replay of the kernel's line accesses per XCD, calibrated against the
+counters): `floor_bytes` is the cold floor, the bytes one launch moves beyond L2 if every XCD fetched each
+X row, scale line and A-stream line it touches exactly once (unbounded L2), plus Y and the partial tiles;
+`floor_frac` = floor_bytes / time / peak. `model` adds the replay's prediction with LRU replacement (what
+the hardware does; it matches the counters) and with optimal replacement (the fewest misses any policy
+could reach on this access order in a 4 MiB L2), and the launch's rate of beyond-L2 requests.
+
 cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over the whole workload, median
 of 5 runs on up to 16 threads (about 10 s of CPU work); plus a single-thread figure over a prefix of SWs
 (~5 s), scaled by panel share.
@@ -189,6 +196,7 @@ def main() -> None:
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-f256", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="skip the L2 traffic model")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (counter calibration)")
     args = ap.parse_args()
@@ -246,6 +254,27 @@ def main() -> None:
         }
         log(f"F{feats}: {ms:.4f} ms/SpMM, {achieved / 1e9:.1f} GB/s algorithmic "
             f"({achieved / HBM_PEAK:.1%} of 8 TB/s), runs {means}")
+
+    if not args.no_model:
+        import model
+        t = time.time()
+        for feats, r in results.items():
+            m = {p: model.traffic(fmt, feats, p, threads=min(16, os.cpu_count() or 1))
+                 for p in ("cold", "lru", "opt")}
+            secs = r["ms"] * 1e-3
+            rl = r["roofline"]
+            rl["floor_bytes"] = m["cold"]["bytes"]
+            rl["floor_frac"] = round(m["cold"]["bytes"] / secs / HBM_PEAK, 4)
+            rl["model"] = {
+                "lru_bytes": m["lru"]["bytes"], "opt_bytes": m["opt"]["bytes"],
+                "cold_bytes": m["cold"]["bytes"],
+                "lru_requests": m["lru"]["requests"],
+                "request_rate_g_per_s": round(m["lru"]["requests"] / secs / 1e9, 2),
+                "misses_lru": m["lru"]["misses"], "misses_opt": m["opt"]["misses"]}
+        log(f"L2 model: {time.time() - t:.1f}s: " + ", ".join(
+            f"F{f} floor {r['roofline']['floor_bytes'] / 1e9:.2f} GB, lru "
+            f"{r['roofline']['model']['lru_bytes'] / 1e9:.2f} GB, opt "
+            f"{r['roofline']['model']['opt_bytes'] / 1e9:.2f} GB" for f, r in results.items()))
 
     base = None
     if not args.no_cpu_baseline:

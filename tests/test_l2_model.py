@@ -1,0 +1,137 @@
+"""The L2 traffic model (model/l2_model.c) against an independent Python replay of the same
+specification on small formats, and the ordering its policies must satisfy."""
+import numpy as np
+import pytest
+
+import model
+import tcc_spmm_amd as T
+
+LINE = 128
+
+
+def _format(cfg="t300_24_5"):
+    csr = T.synth_csr(cfg)
+    return T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+
+
+def _sequence(fmt, features, xcd, xcds, waves):
+    """The model's access order, restated: contiguous task ranges per XCD, `waves` resident tasks
+    taking one panel each in turn; per panel the sourceIds, metadata and values lines, then per
+    real slot its X lines and scale line. Keys are (array, line)."""
+    a = fmt.arrays(copy=False)
+    tasks = [tuple(int(v) for v in t) for t in a["tasks"][["sw", "begin", "end"]]]
+    ids = np.asarray(a["source_ids"])
+    base = (np.asarray(a["source_metadata"])[::8] >> np.uint64(32)).astype(np.int64)
+    n_panels, n_values = base.size, int(a["values"].size)
+    q, r = divmod(len(tasks), xcds)
+    lo = xcd * q + min(xcd, r)
+    queue = [t for t in tasks[lo:lo + q + (1 if xcd < r else 0)] if t[2] > t[1]]
+    slots = [None] * waves
+    for w in range(waves):
+        slots[w] = list(queue.pop(0)[1:]) if queue else None
+    seq = []
+    while any(s is not None for s in slots):
+        for w in range(waves):
+            s = slots[w]
+            if s is None:
+                continue
+            p = s[0]
+            s[0] += 1
+            seq.append((("ids", p * 32 // LINE), "source_ids"))
+            seq.append((("meta", p * 64 // LINE), "metadata"))
+            v0 = int(base[p])
+            v1 = int(base[p + 1]) if p + 1 < n_panels else n_values
+            if v1 > v0:
+                for line in range(v0 * 4 // LINE, (v1 * 4 - 1) // LINE + 1):
+                    seq.append((("val", line), "values"))
+            for k in range(8):
+                src = int(ids[p * 8 + k])
+                if src == 0xFFFFFFFF:
+                    continue
+                for j in range(features // 128):
+                    seq.append((("x", src * (features // 128) + j), "x"))
+                seq.append((("scale", src // 32), "scale"))
+            if s[0] == s[1]:
+                slots[w] = list(queue.pop(0)[1:]) if queue else None
+    return seq
+
+
+def _replay(seq, lines, policy):
+    """Fully associative LRU / optimal (with bypass) / unbounded replay; misses per stream."""
+    misses = {}
+    if policy == "cold":
+        seen = set()
+        for key, st in seq:
+            if key not in seen:
+                seen.add(key)
+                misses[st] = misses.get(st, 0) + 1
+        return misses
+    nxt = [0] * len(seq)
+    last = {}
+    for i in range(len(seq) - 1, -1, -1):
+        nxt[i] = last.get(seq[i][0], 1 << 62)
+        last[seq[i][0]] = i
+    cache = {}  # key -> stamp (LRU: last use; optimal: next use)
+    for i, (key, st) in enumerate(seq):
+        mark = nxt[i] if policy == "opt" else i
+        if key in cache:
+            cache[key] = mark
+            continue
+        misses[st] = misses.get(st, 0) + 1
+        if len(cache) < lines:
+            cache[key] = mark
+            continue
+        if policy == "opt":
+            victim = max(cache, key=cache.get)
+            if mark >= cache[victim]:
+                continue
+        else:
+            victim = min(cache, key=cache.get)
+        del cache[victim]
+        cache[key] = mark
+    return misses
+
+
+@pytest.mark.parametrize("policy", ["lru", "opt", "cold"])
+@pytest.mark.parametrize("features", [128, 256])
+def test_model_matches_an_independent_replay(policy, features):
+    """One set of `lines` ways (fully associative), so the set hash plays no part."""
+    fmt = _format()
+    lines, waves = 64, 6
+    got = model.traffic(fmt, features, policy, waves=waves, l2_bytes=lines * LINE, ways=lines)
+    want = {s: 0 for s in model.STREAMS}
+    for xcd in range(model.XCDS):
+        for st, n in _replay(_sequence(fmt, features, xcd, model.XCDS, waves), lines, policy).items():
+            want[st] += n
+    assert got["misses"] == want
+
+
+def test_policies_are_ordered_and_bytes_add_up():
+    fmt = _format("t2000_30_7")
+    r = {p: model.traffic(fmt, 128, p) for p in ("cold", "opt", "lru")}
+    total = lambda d: sum(d["misses"].values())
+    assert total(r["cold"]) <= total(r["opt"]) <= total(r["lru"])
+    for d in r.values():
+        assert d["bytes"] == LINE * total(d) + 4 * fmt.rows * 128 + 64 * 128 * fmt.partial_count
+        assert d["accesses"] == r["lru"]["accesses"]
+    # every slot of a real source reads one X line and one scale line at F=128
+    ids = np.asarray(fmt.arrays(copy=False)["source_ids"])
+    assert r["lru"]["accesses"]["x"] == int(np.count_nonzero(ids != 0xFFFFFFFF))
+    assert r["lru"]["accesses"]["scale"] == r["lru"]["accesses"]["x"]
+
+
+def test_cold_misses_are_distinct_lines_per_xcd():
+    fmt = _format("t2000_30_7")
+    a = fmt.arrays(copy=False)
+    tasks, ids = a["tasks"], np.asarray(a["source_ids"])
+    q, r = divmod(len(tasks), model.XCDS)
+    want = 0
+    for x in range(model.XCDS):
+        lo = x * q + min(x, r)
+        part = tasks[lo:lo + q + (1 if x < r else 0)]
+        if not len(part):
+            continue
+        src = ids[int(part["begin"][0]) * 8:int(part["end"][-1]) * 8]
+        want += np.unique(src[src != 0xFFFFFFFF]).size
+    got = model.traffic(fmt, 128, "cold")
+    assert got["misses"]["x"] == want
