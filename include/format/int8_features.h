@@ -1,8 +1,9 @@
 // Per-source INT8 feature preparation on the GPU.
 //
 // Drop-in for the reference's include/format/int8_features.cuh:1-15 with hipStream_t in place of
-// cudaStream_t. Callers provide valid, non-aliasing device buffers and non-zero sizes. Launch
-// failures throw std::runtime_error; execution stays asynchronous on `stream`.
+// cudaStream_t. Callers provide valid, non-aliasing device buffers and non-zero sizes. Zero sizes
+// and launch failures throw std::runtime_error; a null buffer throws std::invalid_argument before
+// any launch (the reference launches and faults instead). Execution stays asynchronous on `stream`.
 #pragma once
 #include <hip/hip_runtime_api.h>
 

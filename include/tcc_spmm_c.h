@@ -6,8 +6,9 @@
  * its comment, whose reference declaration is cited. All functions return a status code and never
  * throw: 0 success, 1 std::invalid_argument, 2 std::overflow_error, 3 std::runtime_error (HIP
  * failure or I/O), 4 any other exception. tcc_last_error() returns the message of the last failure
- * on the calling thread. Device entry points are asynchronous on `stream` (a hipStream_t; NULL is
- * the null stream), like the C++ functions they wrap.
+ * on the calling thread. A null handle, output pointer or host input array (one with a nonzero
+ * count) returns 1 before any work. Device entry points are asynchronous on `stream` (a hipStream_t;
+ * NULL is the null stream), like the C++ functions they wrap.
  */
 #ifndef TCC_SPMM_C_H
 #define TCC_SPMM_C_H

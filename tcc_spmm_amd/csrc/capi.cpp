@@ -55,6 +55,11 @@ template <typename Body> int guarded(Body body) {
     }
 }
 
+// A required pointer argument (an output, or an input array with a nonzero count) must not be null.
+void need(const void* p, const char* what) {
+    if (!p) throw std::invalid_argument(std::string("null ") + what);
+}
+
 Sw32DeviceView toView(const tcc_device_view* v) {
     Sw32DeviceView out;
     std::memcpy(static_cast<void*>(&out), v, sizeof(out));
@@ -67,7 +72,10 @@ extern "C" {
 void tccSetLastError(const char* message) { lastError = message ? message : ""; }
 
 int tccWrapCsr(CsrMatrix&& csr, tcc_csr** out) {
-    return guarded([&] { *out = new tcc_csr{std::move(csr)}; });
+    return guarded([&] {
+        need(out, "output handle");
+        *out = new tcc_csr{std::move(csr)};
+    });
 }
 
 const char* tcc_last_error(void) { return lastError.c_str(); }
@@ -77,12 +85,21 @@ const char* tcc_version(void) { return "tcc_spmm_amd 0.1 gfx950"; }
 int tcc_make_canonical_csr(uint32_t rows, uint32_t cols, uint32_t nnz, const uint32_t* rowOffsets,
                            const uint32_t* sourceIds, const float* values, tcc_csr** out) {
     return guarded([&] {
+        need(out, "output handle");
+        need(rowOffsets, "rowOffsets");
+        if (nnz) {
+            need(sourceIds, "sourceIds");
+            need(values, "values");
+        }
         *out = new tcc_csr{makeCanonicalCsr(rows, cols, nnz, rowOffsets, sourceIds, values)};
     });
 }
 
 int tcc_load_matrix_market(const char* path, uint32_t* rows, uint32_t* cols, tcc_csr** out) {
     return guarded([&] {
+        need(rows, "rows");
+        need(cols, "cols");
+        need(out, "output handle");
         MtxMatrix m = loadMatrixMarket(path ? path : "");
         *rows = m.rows;
         *cols = m.cols;
@@ -93,6 +110,12 @@ int tcc_load_matrix_market(const char* path, uint32_t* rows, uint32_t* cols, tcc
 int tcc_csr_from_arrays(uint64_t rowOffsetsCount, const uint32_t* rowOffsets, uint64_t nnz,
                         const uint32_t* sourceIds, const float* values, tcc_csr** out) {
     return guarded([&] {
+        need(out, "output handle");
+        if (rowOffsetsCount) need(rowOffsets, "rowOffsets");
+        if (nnz) {
+            need(sourceIds, "sourceIds");
+            need(values, "values");
+        }
         auto h = std::make_unique<tcc_csr>();
         h->csr.rowOffsets.assign(rowOffsets, rowOffsets + rowOffsetsCount);
         h->csr.sourceIds.assign(sourceIds, sourceIds + nnz);
@@ -104,6 +127,8 @@ int tcc_csr_from_arrays(uint64_t rowOffsetsCount, const uint32_t* rowOffsets, ui
 int tcc_csr_info(const tcc_csr* csr, uint64_t* rowOffsetsCount, uint64_t* nnz) {
     return guarded([&] {
         if (!csr) throw std::invalid_argument("null CSR handle");
+        need(rowOffsetsCount, "rowOffsetsCount");
+        need(nnz, "nnz");
         *rowOffsetsCount = csr->csr.rowOffsets.size();
         *nnz = csr->csr.sourceIds.size();
     });
@@ -113,6 +138,9 @@ int tcc_csr_arrays(const tcc_csr* csr, const uint32_t** rowOffsets, const uint32
                    const float** values) {
     return guarded([&] {
         if (!csr) throw std::invalid_argument("null CSR handle");
+        need(rowOffsets, "rowOffsets");
+        need(sourceIds, "sourceIds");
+        need(values, "values");
         *rowOffsets = csr->csr.rowOffsets.data();
         *sourceIds = csr->csr.sourceIds.data();
         *values = csr->csr.values.data();
@@ -125,6 +153,7 @@ int tcc_convert_csr_to_sw32(uint32_t rows, uint32_t cols, const tcc_csr* csr, in
                             tcc_sw32** out) {
     return guarded([&] {
         if (!csr) throw std::invalid_argument("null CSR handle");
+        need(out, "output handle");
         *out = new tcc_sw32{convertCsrToSw32(rows, cols, csr->csr, bucketByRwMask != 0)};
     });
 }
@@ -139,6 +168,7 @@ int tcc_build_panel_tasks(tcc_sw32* format) {
 int tcc_sw32_get_sizes(const tcc_sw32* format, tcc_sw32_sizes* s) {
     return guarded([&] {
         if (!format) throw std::invalid_argument("null SW32 handle");
+        need(s, "sizes");
         const Sw32HostFormat& f = format->format;
         s->rows = f.rows;
         s->cols = f.cols;
@@ -159,6 +189,7 @@ int tcc_sw32_get_sizes(const tcc_sw32* format, tcc_sw32_sizes* s) {
 int tcc_sw32_get_arrays(const tcc_sw32* format, tcc_sw32_arrays* a) {
     return guarded([&] {
         if (!format) throw std::invalid_argument("null SW32 handle");
+        need(a, "arrays");
         const Sw32HostFormat& f = format->format;
         a->windowOffsets = f.windowOffsets.data();
         a->sourceIds = f.sourceIds.data();
@@ -213,6 +244,7 @@ int tcc_device_matrix_create(const tcc_sw32* format, uint32_t features, tcc_devi
         if (!format) throw std::invalid_argument("null SW32 handle");
         if (format->format.bucketOffsets.empty())
             throw std::invalid_argument("device matrices need the RW-bucketed SW32 format");
+        need(out, "output handle");
         auto m = std::make_unique<DeviceMatrix>(format->format, features);
         *out = new tcc_device_matrix{std::move(m)};
     });
@@ -222,6 +254,9 @@ int tcc_device_matrix_view(const tcc_device_matrix* m, tcc_device_view* view, fl
                            uint32_t** counters) {
     return guarded([&] {
         if (!m || !m->matrix) throw std::invalid_argument("null device matrix");
+        need(view, "view");
+        need(partials, "partials");
+        need(counters, "counters");
         const Sw32DeviceView v = m->matrix->view();
         std::memcpy(static_cast<void*>(view), &v, sizeof(v));
         const SpmmWorkspace w = m->matrix->workspace();

@@ -152,6 +152,8 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
                           std::uint32_t features, hipStream_t stream) {
     // A zero-sized grid is a launch error, reported like the runtime would (std::runtime_error).
     if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
+    // A null buffer would fault the GPU; rejected before any launch (the reference does not check).
+    if (!x || !q || !scale) throw std::invalid_argument("quantize: null device buffer");
     const bool vector = features % 4 == 0 && reinterpret_cast<std::uintptr_t>(x) % 16 == 0 &&
                         reinterpret_cast<std::uintptr_t>(q) % 4 == 0;
     if (vector) {
@@ -190,6 +192,7 @@ void packFeaturesInt8x16(const std::int8_t* q, std::int8_t* packed, std::uint32_
                          std::uint32_t features, hipStream_t stream) {
     if (!sources || !features) throw std::runtime_error("pack: invalid configuration argument");
     if (features % 16) throw std::invalid_argument("packed16 needs features % 16 == 0");
+    if (!q || !packed) throw std::invalid_argument("pack: null device buffer");
     const std::size_t bytes = std::size_t(sources) * features;
     const bool aligned = (reinterpret_cast<std::uintptr_t>(q) % 16 == 0) &&
                          (reinterpret_cast<std::uintptr_t>(packed) % 16 == 0);

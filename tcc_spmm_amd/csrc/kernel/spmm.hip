@@ -756,19 +756,37 @@ void launch(const KernelArgs& args, hipStream_t stream) {
 
 } // namespace
 
+namespace {
+
+// Checks shared by both entry points, before anything is launched. Null buffers would fault the GPU
+// and are rejected (the reference does not check). Of the view, only the arrays every plan has are
+// required (tasks, and bucketOffsets with 17 entries per SW): a plan without panels has empty
+// sourceIds, sourceMetadata and values, which may be null. The workspace may be null (a plan
+// without split SWs), and its size is the caller's contract.
+void checkLaunchArguments(const Sw32DeviceView& matrix, const std::int8_t* packedX,
+                          const float* scales, const float* output) {
+    if (!matrix.taskCount)
+        throw std::runtime_error("launchSpmmInt8: invalid configuration argument (no tasks)");
+    if (matrix.taskCount > 0x7FFFFFFFu)
+        throw std::invalid_argument("launchSpmmInt8: too many tasks for one launch");
+    if (!packedX || !scales || !output)
+        throw std::invalid_argument("launchSpmmInt8: null packedX, scales or output");
+    if (!matrix.tasks || !matrix.bucketOffsets)
+        throw std::invalid_argument("launchSpmmInt8: device view with null tasks or bucketOffsets");
+    // The packed features are read as u16 pairs at least (reference include/format/int8_features.cuh:
+    // 11-13 states u16 alignment); an odd address cannot be.
+    if (reinterpret_cast<std::uintptr_t>(packedX) % 2)
+        throw std::invalid_argument("launchSpmmInt8: packedX must be u16-aligned");
+}
+
+} // namespace
+
 void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
                     float* output, std::uint32_t rows, std::uint32_t cols, std::uint32_t features,
                     SpmmWorkspace workspace, hipStream_t stream) {
     if (features != 128 && features != 256)
         throw std::invalid_argument("feature dimension must be 128 or 256");
-    if (!matrix.taskCount)
-        throw std::runtime_error("launchSpmmInt8: invalid configuration argument (no tasks)");
-    if (matrix.taskCount > 0x7FFFFFFFu)
-        throw std::invalid_argument("launchSpmmInt8: too many tasks for one launch");
-    // The packed features are read as u16 pairs at least (reference include/format/int8_features.cuh:
-    // 11-13 states u16 alignment); an odd address cannot be.
-    if (reinterpret_cast<std::uintptr_t>(packedX) % 2)
-        throw std::invalid_argument("launchSpmmInt8: packedX must be u16-aligned");
+    checkLaunchArguments(matrix, packedX, scales, output);
     const KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
                           rows,   cols};
     if (features == 128)
@@ -822,6 +840,7 @@ void launchSpmmInt8NoAlloc(Sw32DeviceView matrix, const std::int8_t* packedX, co
                            std::uint32_t features, std::uint32_t partialCount, hipStream_t stream) {
     if (features != 128 && features != 256)
         throw std::invalid_argument("feature dimension must be 128 or 256");
+    checkLaunchArguments(matrix, packedX, scales, output);
     SpmmWorkspace workspace;
     if (partialCount) {
         const std::uint64_t counters = (std::uint64_t(rows) + 31) / 32 * (features / 128);

@@ -95,23 +95,106 @@ def test_header_structs_match_cpp_layouts():
     assert "static_assert(sizeof(Sw32Task) == 28" in header
 
 
+# A non-null address the host never dereferences: the checks that see it reject the call before
+# any launch or copy.
+PLACEHOLDER = 0x1000
+
+
+def _placeholder_view():
+    from tcc_spmm_amd._lib import DeviceView
+    view = DeviceView()
+    for name, _ in DeviceView._fields_:
+        if name != "taskCount":
+            setattr(view, name, PLACEHOLDER)
+    view.taskCount = 1
+    return view
+
+
+def test_device_entry_points_reject_null_buffers_before_any_launch():
+    """A null device buffer would fault the GPU: the launch, quantize and pack entry points reject
+    it with TCC_INVALID_ARGUMENT first, so this runs on a CPU-only host."""
+    from tcc_spmm_amd._lib import DeviceView, lib
+    L, P = lib(), PLACEHOLDER
+    view = _placeholder_view()
+    for args in ((None, P, P), (P, None, P), (P, P, None)):
+        st = L.tcc_launch_spmm_int8(ctypes.byref(view), *args, 32, 32, 128, None, None, None)
+        assert st == 1 and b"null" in L.tcc_last_error()
+        st = L.tcc_launch_spmm_int8_noalloc(ctypes.byref(view), *args, 32, 32, 128, 0, None)
+        assert st == 1 and b"null" in L.tcc_last_error()
+    bad = _placeholder_view()
+    bad.tasks = None
+    st = L.tcc_launch_spmm_int8(ctypes.byref(bad), P, P, P, 32, 32, 256, None, None, None)
+    assert st == 1 and b"null tasks" in L.tcc_last_error()
+    for args in ((None, P, P), (P, None, P), (P, P, None)):
+        st = L.tcc_quantize_features_int8(*args, 4, 128, None)
+        assert st == 1 and b"null" in L.tcc_last_error()
+    for args in ((None, P), (P, None)):
+        st = L.tcc_pack_features_int8x16(*args, 4, 128, None)
+        assert st == 1 and b"null" in L.tcc_last_error()
+
+
 def test_noalloc_entry_point_rejects_before_any_launch():
     """launchSpmmInt8NoAlloc checks the feature count and the size of the plan's workspace against
     its fixed scratch before touching the GPU, so both rejections run on a CPU-only host."""
     from tcc_spmm_amd._lib import DeviceView, lib
-    view = DeviceView()
-    view.taskCount = 1
+    view = _placeholder_view()
     st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 32, 32, 64, 1,
                                             None)
     assert st == 1 and b"128 or 256" in lib().tcc_last_error()
+    # Placeholder addresses pass the null checks; the size check rejects before anything reads them.
+    x, sc, y = PLACEHOLDER, PLACEHOLDER, PLACEHOLDER
     # c3 at F=256: 14,731 partial tiles of 8 KiB need 120.7 MB, more than the 64 MiB scratch.
-    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 2449029,
-                                            2449029, 256, 14731, None)
+    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), x, sc, y, 2449029, 2449029, 256,
+                                            14731, None)
     assert st == 1 and b"scratch" in lib().tcc_last_error()
     # The largest plan that fits at F=128 for 4096 rows: 128 counters (one 256-byte block) plus
     # K tiles of 4 KiB in 64 MiB.
     k_max = ((64 << 20) - 256) // (8 * 128 * 4)
-    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), None, None, None, 4096, 4096, 128,
+    st = lib().tcc_launch_spmm_int8_noalloc(ctypes.byref(view), x, sc, y, 4096, 4096, 128,
                                             k_max + 1, None)
     assert st == 1 and b"scratch" in lib().tcc_last_error()
     assert b"noalloc" in (ROOT / "include" / "tcc_spmm_c.h").read_bytes()
+
+
+def test_null_outputs_and_arrays_are_rejected():
+    """A null output pointer, handle or input array returns TCC_INVALID_ARGUMENT (1) instead of
+    crashing the caller; these are host-only entry points, so this runs on a CPU-only host."""
+    import numpy as np
+    from tcc_spmm_amd._lib import Sw32Sizes, lib
+    L = lib()
+    offsets = np.array([0, 1, 2], np.uint32)
+    ids = np.array([0, 1], np.uint32)
+    vals = np.array([1.0, 2.0], np.float32)
+    h = ctypes.c_void_p()
+    u32 = ctypes.c_uint32()
+
+    def rejected(status, what):
+        assert status == 1, what
+        assert b"null" in L.tcc_last_error(), what
+
+    rejected(L.tcc_make_canonical_csr(2, 2, 2, offsets.ctypes.data, ids.ctypes.data,
+                                      vals.ctypes.data, None), "make_canonical_csr out")
+    rejected(L.tcc_make_canonical_csr(2, 2, 2, None, ids.ctypes.data, vals.ctypes.data,
+                                      ctypes.byref(h)), "make_canonical_csr rowOffsets")
+    rejected(L.tcc_make_canonical_csr(2, 2, 2, offsets.ctypes.data, None, vals.ctypes.data,
+                                      ctypes.byref(h)), "make_canonical_csr sourceIds")
+    rejected(L.tcc_csr_from_arrays(3, offsets.ctypes.data, 2, None, vals.ctypes.data,
+                                   ctypes.byref(h)), "csr_from_arrays sourceIds")
+    rejected(L.tcc_load_matrix_market(b"x.mtx", None, ctypes.byref(u32), ctypes.byref(h)),
+             "load_matrix_market rows")
+    assert L.tcc_make_canonical_csr(2, 2, 2, offsets.ctypes.data, ids.ctypes.data,
+                                    vals.ctypes.data, ctypes.byref(h)) == 0
+    try:
+        rejected(L.tcc_csr_info(h, None, None), "csr_info")
+        rejected(L.tcc_convert_csr_to_sw32(2, 2, h, 1, None), "convert out")
+        fmt = ctypes.c_void_p()
+        assert L.tcc_convert_csr_to_sw32(2, 2, h, 1, ctypes.byref(fmt)) == 0
+        try:
+            rejected(L.tcc_sw32_get_sizes(fmt, None), "sw32_get_sizes")
+            rejected(L.tcc_sw32_get_arrays(fmt, None), "sw32_get_arrays")
+            sizes = Sw32Sizes()
+            assert L.tcc_sw32_get_sizes(fmt, ctypes.byref(sizes)) == 0 and sizes.rows == 2
+        finally:
+            L.tcc_sw32_free(fmt)
+    finally:
+        L.tcc_csr_free(h)
