@@ -91,12 +91,28 @@ def pack_features_int8x16(q: torch.Tensor, packed: torch.Tensor | None = None, s
     return packed
 
 
-def _check_operands(packed_x, scales, output, rows: int, cols: int, features: int) -> None:
+def _check_operands(packed_x, scales, output, rows: int, cols: int, features: int,
+                    workspace=None) -> None:
+    """Layout and size first, then the device, so that every rejection happens before a launch.
+
+    Of the workspace contract (reference include/spmm.cuh:5-13) the view leaves these checkable:
+    partials are contiguous float32; counters are contiguous int32 with ceil(rows/32) *
+    features/128 elements. The partial count is the plan's, so sizing the partials is the caller's.
+    """
     _require_buffer(packed_x, "packed_x", torch.int8, cols * features)
     _require_buffer(scales, "scales", torch.float32, cols)
     _require_buffer(output, "output", torch.float32, rows * features)
-    _require_cuda(packed_x, scales, output)
-    _require_same_device(packed_x.device, scales, output)
+    partials = counters = None
+    if workspace is not None:
+        partials, counters = workspace.partials, workspace.counters
+        if partials is not None and (partials.dtype != torch.float32 or
+                                     not partials.is_contiguous()):
+            raise ValueError("workspace partials must be a contiguous float32 tensor")
+        if counters is not None:
+            _require_buffer(counters, "workspace counters", torch.int32,
+                            (rows + 31) // 32 * max(features // 128, 1))
+    _require_cuda(packed_x, scales, output, partials, counters)
+    _require_same_device(packed_x.device, scales, output, partials, counters)
 
 
 @dataclass
@@ -114,11 +130,12 @@ def launch_spmm_int8(view: DeviceView, packed_x: torch.Tensor, scales: torch.Ten
 
     Raises ValueError before any launch unless packed_x (int8, >= cols * features elements),
     scales (float32, >= cols) and output (float32, >= rows * features) are contiguous tensors on
-    one GPU; the feature count itself is checked by the library (128 or 256, invalid_argument).
+    one GPU, with a workspace (when given) of contiguous float32 partials and int32 counters of at
+    least ceil(rows/32) * features/128 elements on that GPU; the feature count itself is checked by
+    the library (128 or 256, invalid_argument).
     """
-    _check_operands(packed_x, scales, output, rows, cols, features)
     ws = workspace or SpmmWorkspace(None, None)
-    _require_same_device(packed_x.device, ws.partials, ws.counters)
+    _check_operands(packed_x, scales, output, rows, cols, features, ws)
     check(lib().tcc_launch_spmm_int8(C.byref(view), _ptr(packed_x), _ptr(scales), _ptr(output),
                                      rows, cols, features, _ptr(ws.partials), _ptr(ws.counters),
                                      _stream_ptr(stream)))
@@ -197,6 +214,8 @@ class NativeDeviceMatrix:
         check(lib().tcc_device_matrix_view(self._h, C.byref(self.view), C.byref(p), C.byref(c)))
         self.partials_ptr, self.counters_ptr = p.value or 0, c.value or 0
         self.rows, self.cols, self.features = fmt.rows, fmt.cols, features
+        # The library uploads to the device current at creation.
+        self.device = torch.device("cuda", torch.cuda.current_device())
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -206,6 +225,7 @@ class NativeDeviceMatrix:
     def spmm(self, packed_x: torch.Tensor, scales: torch.Tensor, output: torch.Tensor,
              stream=None) -> torch.Tensor:
         _check_operands(packed_x, scales, output, self.rows, self.cols, self.features)
+        _require_same_device(self.device, packed_x)
         check(lib().tcc_launch_spmm_int8(C.byref(self.view), _ptr(packed_x), _ptr(scales),
                                          _ptr(output), self.rows, self.cols, self.features,
                                          self.partials_ptr, self.counters_ptr,

@@ -54,6 +54,19 @@ def test_launch_accepts_larger_buffers_before_the_device_check():
         _launch(packed, scales, out, SpmmWorkspace(None, None))
 
 
+@pytest.mark.parametrize("partials,counters,match", [
+    (torch.zeros(8 * F, dtype=torch.float64), None, "partials must be a contiguous float32"),
+    (torch.zeros((F, 8), dtype=torch.float32).t(), None, "partials must be a contiguous float32"),
+    (None, torch.zeros(2, dtype=torch.int64), "counters must be torch.int32"),
+    # ceil(40 / 32) = 2 SWs, one counter each at F = 128
+    (None, torch.zeros(1, dtype=torch.int32), "counters holds 1 elements, needs at least 2"),
+    (torch.zeros(8 * F, dtype=torch.float32), torch.zeros(2, dtype=torch.int32), "CUDA"),
+])
+def test_launch_rejects_malformed_workspace(partials, counters, match):
+    with pytest.raises(ValueError, match=match):
+        _launch(*_operands(), SpmmWorkspace(partials, counters))
+
+
 @pytest.mark.parametrize("q,scale,match", [
     (torch.zeros((COLS, F), dtype=torch.uint8), None, "q must be torch.int8"),
     (torch.zeros((COLS, F - 1), dtype=torch.int8), None, "q holds"),
