@@ -49,6 +49,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -618,28 +619,66 @@ __device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
     return xcd * q + min(xcd, r) + j;
 }
 
-// One task over all S = Features / 128 slices of its SW (one wave).
-template <unsigned Features, unsigned Addr>
+// One task over all S = Features / 128 slices of its SW, by `Waves` waves of one workgroup. With
+// more than one wave, wave w walks the w-th of `Waves` equal shares of the task's panels (its own
+// LDS tables, the same walk as a whole task), then hands its accumulators to wave 0, which adds them
+// in wave order and finishes the task alone. A task then takes about 1/Waves of the time, which
+// shortens launches whose longest tasks set the time (few tasks per wave slot).
+template <unsigned Features, unsigned Addr, unsigned Waves = 1>
 __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex) {
     constexpr unsigned S = Features / kSlice;
-    __shared__ __align__(16) _Float16 table16[256];
-    __shared__ __align__(16) float table32[256];
-    __shared__ __align__(16) u32x4 xtile[64 * S];
-    __shared__ __align__(16) float mant[8];
-    __shared__ unsigned short redo[384];
+    __shared__ __align__(16) _Float16 table16[Waves][256];
+    __shared__ __align__(16) float table32[Waves][256];
+    __shared__ __align__(16) u32x4 xtile[Waves][64 * S];
+    __shared__ __align__(16) float mant[Waves][8];
+    __shared__ unsigned short redo[Waves][384];
     __shared__ unsigned lastFlag[S];
-    const unsigned lane = threadIdx.x;
+    const unsigned wave = Waves == 1 ? 0u : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const unsigned lane = Waves == 1 ? threadIdx.x : threadIdx.x & 63u;
     const Sw32Task task = a.m.tasks[taskIndex];
     const unsigned sw = task.sw;
     const Loader<Addr> ld(a, task.begin, task.end, Features);
-    const Lds lds{table16, table32, xtile, mant, redo};
+    const Lds lds{table16[wave], table32[wave], xtile[wave], mant[wave], redo[wave]};
 
     f32x16 acc[4 * S];
 #pragma unroll
     for (unsigned b = 0; b < 4 * S; ++b) acc[b] = f32x16{};
-    walkTask<S>(ld, a.m.bucketOffsets + std::size_t(sw) * 17, task.begin, task.end, lane, lds, acc);
+    unsigned lo = task.begin, hi = task.end;
+    if constexpr (Waves > 1) {
+        const std::uint64_t n = hi - lo;
+        lo = task.begin + unsigned(n * wave / Waves);
+        hi = task.begin + unsigned(n * (wave + 1) / Waves);
+    }
+    walkTask<S>(ld, a.m.bucketOffsets + std::size_t(sw) * 17, lo, hi, lane, lds, acc);
 #pragma unroll
     for (unsigned b = 0; b < 4 * S; ++b) acc[b] *= 2.0f; // Y / 2 to Y, exact
+    if constexpr (Waves > 1) {
+        // One accumulator block (16 floats per lane) per round, as four 16-byte chunks per lane
+        // laid out chunk-major so that each chunk's 64 lanes are contiguous.
+        __shared__ __align__(16) f32x4 handoff[Waves - 1][4][kWave];
+#pragma unroll
+        for (unsigned b = 0; b < 4 * S; ++b) {
+            if (wave != 0) {
+#pragma unroll
+                for (unsigned q = 0; q < 4; ++q)
+                    handoff[wave - 1][q][lane] =
+                        f32x4{acc[b][4 * q], acc[b][4 * q + 1], acc[b][4 * q + 2], acc[b][4 * q + 3]};
+            }
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (unsigned v = 0; v + 1 < Waves; ++v)
+#pragma unroll
+                    for (unsigned q = 0; q < 4; ++q) {
+                        const f32x4 o = handoff[v][q][lane];
+#pragma unroll
+                        for (unsigned e = 0; e < 4; ++e) acc[b][4 * q + e] += o[e];
+                    }
+            }
+            __syncthreads();
+        }
+        if (wave != 0) return;
+    }
 
     const unsigned row = lane & 31, h = lane >> 5;
     auto sub = [&](unsigned k) -> const f32x16(&)[4] {
@@ -710,20 +749,38 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
 
 // F128: four waves per SIMD; the 64 accumulators live in ordinary VGPRs and the kernel fits 128
 // registers.
-template <unsigned Addr>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(4, 8))) void spmmInt8Kernel128(
-    KernelArgs a) {
-    runTask<128, Addr>(a, xcdTask(blockIdx.x, a.m.taskCount));
+template <unsigned Addr, unsigned Waves = 1>
+__global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(4, 8))) void
+spmmInt8Kernel128(KernelArgs a) {
+    runTask<128, Addr, Waves>(a, xcdTask(blockIdx.x, a.m.taskCount));
 }
 
 // F256: both 128-feature slices of a task in one wave (128 accumulator registers, two waves per
 // SIMD). The task's A stream, scales and A table are read and built once for both slices; measured
 // on c3 this moves 18% fewer bytes (33.1 GB against 40.5 GB) and runs 8.6% faster than one wave
 // per (task, slice).
-template <unsigned Addr>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2, 8))) void spmmInt8Kernel256(
-    KernelArgs a) {
-    runTask<256, Addr>(a, xcdTask(blockIdx.x, a.m.taskCount));
+template <unsigned Addr, unsigned Waves = 1>
+__global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(2, 8))) void
+spmmInt8Kernel256(KernelArgs a) {
+    runTask<256, Addr, Waves>(a, xcdTask(blockIdx.x, a.m.taskCount));
+}
+
+// Waves per task: 2 when the plan has few tasks for the chip's wave slots, so that the longest
+// tasks, not the bandwidth, set the launch time; else 1. Measured crossovers on MI355X (256 CUs;
+// wave slots = CUs x 4 SIMDs x the kernel's waves per SIMD, 4 at F128 and 2 at F256): F128 gains
+// below about 3 tasks per slot (-39% at 250 tasks, -6% at 8,790, even at 12,500, +3% at 38,281),
+// F256 below about half a task per slot (-26% at 1,000 tasks, +1% at 1,875). TCC_SPMM_TASK_WAVES=1
+// or 2 overrides the choice (tests and measurements).
+unsigned taskWaves(unsigned taskCount, unsigned features) {
+    if (const char* forced = std::getenv("TCC_SPMM_TASK_WAVES"))
+        return std::strcmp(forced, "2") == 0 ? 2u : 1u;
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        return 1;
+    const std::uint64_t slots = std::uint64_t(cus) * 4 * (features == 128 ? 4 : 2);
+    const std::uint64_t limit = features == 128 ? 3 * slots : slots / 2;
+    return taskCount < limit ? 2u : 1u;
 }
 
 template <unsigned Features>
@@ -737,11 +794,17 @@ void launch(const KernelArgs& args, hipStream_t stream) {
                       std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
     const dim3 grid(args.m.taskCount, 1);
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kWave), 0, stream, args); };
+    auto go2 = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(2 * kWave), 0, stream, args);
+    };
+    const bool split = !misaligned && !wide && taskWaves(args.m.taskCount, Features) == 2;
     if constexpr (Features == 256) {
         if (misaligned)
             go(spmmInt8Kernel256<kGlobalU16>);
         else if (wide)
             go(spmmInt8Kernel256<kGlobal>);
+        else if (split)
+            go2(spmmInt8Kernel256<kBuffer, 2>);
         else
             go(spmmInt8Kernel256<kBuffer>);
     } else {
@@ -749,6 +812,8 @@ void launch(const KernelArgs& args, hipStream_t stream) {
             go(spmmInt8Kernel128<kGlobalU16>);
         else if (wide)
             go(spmmInt8Kernel128<kGlobal>);
+        else if (split)
+            go2(spmmInt8Kernel128<kBuffer, 2>);
         else
             go(spmmInt8Kernel128<kBuffer>);
     }

@@ -92,6 +92,37 @@ def test_spmm_c2_full(oracle, gpu, feats):
     assert_close(y, y_ref, f"c2 F{feats}")
 
 
+@pytest.mark.parametrize("waves", ["1", "2"])
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_both_task_forms(oracle, golden, gpu, feats, waves, monkeypatch):
+    """Each task form whatever the launch would pick (TCC_SPMM_TASK_WAVES): one wave per task, or
+    the task's panels shared by two waves whose accumulators wave 0 adds in wave order. On the
+    split and bucket-edge golden cases and on c2: Y within tolerance of the oracle, counters back to
+    zero (checked by _run), and a repeated launch bitwise identical."""
+    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", waves)
+    for case in ("empty_all", "single", "tail_33", "long_shared", "panels_384", "panels_385",
+                 "split_mixed", "split_two"):
+        rows, cols = (int(x) for x in golden[f"{case}/dims"])
+        off, src, val = (golden[f"{case}/csr_offsets"], golden[f"{case}/csr_sources"],
+                         golden[f"{case}/csr_values"])
+        fmt = T.convert_csr_to_sw32(rows, cols, T.make_canonical_csr(rows, cols, off, src, val))
+        x = features(cols, feats, seed=rows + 7 * cols, stddev=2.0)
+        packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+        _, y = _run(fmt, packed, scale, feats, gpu)
+        _, y_again = _run(fmt, packed, scale, feats, gpu)
+        assert np.array_equal(y.view(np.uint32), y_again.view(np.uint32)), case
+        y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
+        assert_close(y, y_ref, f"{case} F{feats} waves {waves}")
+    csr = T.synth_csr("c2")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, feats, seed=302)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    y_ref = oracle.spmm_csr_f64(csr.rows, csr.row_offsets, csr.source_ids, csr.values, pk, sc,
+                                csr.cols)
+    assert_close(y, y_ref, f"c2 F{feats} waves {waves}")
+
+
 def _check_windows(oracle, csr, fmt, y, pk, sc, windows, what, conditioned=False):
     of = oracle.sw32(csr.rows, csr.cols, *csr.views())
     y_ref, y_abs = of.spmm_windows_f64(pk, sc, windows, with_abs=True)
@@ -332,12 +363,14 @@ def test_spmm_huge_a_values_stay_finite(oracle, gpu, feats):
 
 
 @pytest.mark.parametrize("feats", [128, 256])
-def test_spmm_u16_aligned_packed_x(oracle, golden, gpu, feats):
+def test_spmm_u16_aligned_packed_x(oracle, golden, gpu, feats, monkeypatch):
     """packedX need only be u16-aligned, as in the reference (include/format/int8_features.cuh:11-13):
     packed features placed 2, 6 and 14 bytes past a 16-byte boundary give Y bitwise equal to the
-    aligned launch; an odd address raises invalid_argument before any launch."""
+    aligned launch; an odd address raises invalid_argument before any launch. (The u16 instance
+    runs one wave per task, so the aligned launch is held to one wave as well.)"""
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix
+    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", "1")
     for case in ("tail_33", "all_masks", "split_mixed", "random_3"):
         rows, cols = (int(v) for v in golden[f"{case}/dims"])
         off, src, val = (golden[f"{case}/csr_offsets"], golden[f"{case}/csr_sources"],
@@ -385,7 +418,9 @@ def test_quantize_subnormal_and_huge_rows_bit_exact(oracle, gpu):
 @pytest.mark.parametrize("feats", [128, 256])
 def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
     """The 64-bit-addressing kernel instance (taken when packed X exceeds 32-bit byte offsets) gives
-    the same Y as the buffer-addressed one."""
+    the same Y as the buffer-addressed one (both at one wave per task, the wide instance's only
+    form)."""
+    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", "1")
     for case in ("single", "tail_33", "all_masks", "long_shared", "panels_385", "split_mixed",
                  "split_two", "random_3"):
         rows, cols = (int(x) for x in golden[f"{case}/dims"])
