@@ -1,11 +1,13 @@
 // Fused INT8-dequantization SpMM for MI355X (gfx950, wave64): Y = A x tf32(dequant(X)).
 //
 // Work decomposition
-//   One wavefront per workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW). The wave
-//   walks the task's panels once, in order, and accumulates all 32 rows x F features of the SW:
-//   four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block; M =
-//   features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per slice.
-//   F256 runs both slices in the same wave, so the A side of a panel is loaded and built once.
+//   One workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW), normally one wavefront.
+//   The wave walks the task's panels once, in order, and accumulates all 32 rows x F features of
+//   the SW: four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block;
+//   M = features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per
+//   slice. F256 runs both slices in the same wave, so the A side of a panel is loaded and built
+//   once. Plans with few tasks for the chip take two waves per task instead, each walking half the
+//   panels, with the second wave's accumulators added by the first (runTask).
 //
 // Operands of one panel
 //   A (features x slots): the 8 slot rows of the X slice are gathered with one dwordx4 load per
