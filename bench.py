@@ -82,17 +82,23 @@ def time_launches(dm, packed, scale, y, steps, warmup, stream):
 
 
 def time_feature_prep(x, xq, scale, packed, stream, reps=5):
-    """quantizeFeaturesInt8 and packFeaturesInt8x16 on resident buffers: ms per call (median of `reps`
-    event-timed calls on `stream`) and HBM-roofline fraction of their algorithmic bytes."""
+    """quantizeFeaturesInt8, packFeaturesInt8x16 and the fused quantizePackFeaturesInt8 on resident
+    buffers: ms per call (median of `reps` event-timed calls on `stream`) and HBM-roofline fraction of
+    their algorithmic bytes."""
     import torch
-    from tcc_spmm_amd.device import pack_features_int8x16, quantize_features_int8
+    from tcc_spmm_amd.device import (pack_features_int8x16, quantize_features_int8,
+                                     quantize_pack_features_int8)
     out = {}
     sources, features = x.shape
     for name, fn, nbytes in (
             ("quantize", lambda: quantize_features_int8(x, xq, scale, stream=stream),
              sources * (4 * features + features + 4)),
             ("pack", lambda: pack_features_int8x16(xq, packed, stream=stream),
-             2 * sources * features)):
+             2 * sources * features),
+            # the fused form writes the same packed bytes and scales (bit-identical), so the
+            # SpMM inputs are unchanged
+            ("quantize_pack", lambda: quantize_pack_features_int8(x, packed, scale, stream=stream),
+             sources * (4 * features + features + 4))):
         fn()
         times = []
         for _ in range(reps):

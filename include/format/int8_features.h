@@ -21,3 +21,13 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
 // (reference int8_features.cuh:11-15)
 void packFeaturesInt8x16(const std::int8_t* q, std::int8_t* packed, std::uint32_t sources,
                          std::uint32_t features, hipStream_t stream = nullptr);
+
+// quantizeFeaturesInt8 followed by packFeaturesInt8x16 in one pass, with no counterpart in the
+// reference: `packed` and `scale` are bit for bit what that pair of calls writes, but the
+// quantized bytes go straight to the packed layout, so X is read once and nothing else is written
+// (5F + 4 bytes per source instead of 7F + 4). For callers that quantize X for every SpMM.
+// Features must be a multiple of 16 (std::invalid_argument); zero sizes throw std::runtime_error and
+// null buffers std::invalid_argument, before any launch. `packed` must not alias x.
+void quantizePackFeaturesInt8(const float* x, std::int8_t* packed, float* scale,
+                              std::uint32_t sources, std::uint32_t features,
+                              hipStream_t stream = nullptr);

@@ -109,6 +109,10 @@ int tcc_quantize_features_int8(const float* x, int8_t* q, float* scale, uint32_t
 /* packFeaturesInt8x16 — reference include/format/int8_features.cuh:14-15. */
 int tcc_pack_features_int8x16(const int8_t* q, int8_t* packed, uint32_t sources, uint32_t features,
                               void* stream);
+/* quantizePackFeaturesInt8 (include/format/int8_features.h) — no counterpart in the reference: the
+ * two calls above in one pass, bit-identical output, for callers that quantize X for every SpMM. */
+int tcc_quantize_pack_features_int8(const float* x, int8_t* packed, float* scale, uint32_t sources,
+                                    uint32_t features, void* stream);
 
 /* DeviceMatrix — reference src/device_matrix.cuh:8-37: uploads every array of a bucketed format,
  * allocates partials (partialCount*8*features floats) and counters (nSW*(features/128) uint32,

@@ -78,6 +78,8 @@ SIGNATURES = {
                                              C.c_uint32, C.c_void_p]),
     "tcc_pack_features_int8x16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
                                             C.c_void_p]),
+    "tcc_quantize_pack_features_int8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32,
+                                                  C.c_uint32, C.c_void_p]),
     "tcc_device_matrix_create": (C.c_int, [C.c_void_p, C.c_uint32, C.POINTER(C.c_void_p)]),
     "tcc_device_matrix_view": (C.c_int, [C.c_void_p, C.POINTER(DeviceView),
                                          C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),

@@ -239,6 +239,14 @@ int tcc_pack_features_int8x16(const int8_t* q, int8_t* packed, uint32_t sources,
     });
 }
 
+int tcc_quantize_pack_features_int8(const float* x, int8_t* packed, float* scale, uint32_t sources,
+                                    uint32_t features, void* stream) {
+    return guarded([&] {
+        quantizePackFeaturesInt8(x, packed, scale, sources, features,
+                                 static_cast<hipStream_t>(stream));
+    });
+}
+
 int tcc_device_matrix_create(const tcc_sw32* format, uint32_t features, tcc_device_matrix** out) {
     return guarded([&] {
         if (!format) throw std::invalid_argument("null SW32 handle");

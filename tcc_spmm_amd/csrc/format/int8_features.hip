@@ -10,6 +10,12 @@
 // pack: one thread per 16-byte tile; four v_perm_b32 byte shuffles turn q[0..15] into
 // [q0,q8,q1,q9,...,q7,q15] (reference src/format/pack_int8.cu:6-15). Unaligned buffers use a
 // byte-pair kernel with the same result.
+//
+// quantize + pack fused (no counterpart in the reference): the quantize kernels with `Packed` set
+// write the packed layout directly, so q is never written and read back. In the vector kernels the
+// four lanes of a 16-feature tile swap their quantized dwords with two quad-permute DPP moves and
+// assemble their output dword with one v_perm_b32; the scalar kernel stores each byte at its packed
+// position.
 #include "format/int8_features.h"
 #include "hip_support.h"
 
@@ -23,6 +29,14 @@ namespace {
 constexpr unsigned kWave = 64;
 constexpr unsigned kRowsPerBlock = 4;
 
+// Byte offset of feature j of a row in the packed16 layout: within each 16-feature tile, feature k
+// goes to byte 2k (k < 8) or 2(k - 8) + 1.
+__device__ __forceinline__ unsigned packedOffset(unsigned j) {
+    const unsigned k = j & 15u;
+    return (j & ~15u) + (k < 8 ? 2 * k : 2 * (k - 8) + 1);
+}
+
+template <bool Packed>
 __global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
     const float* __restrict__ x, std::int8_t* __restrict__ q, float* __restrict__ scale,
     unsigned sources, unsigned features) {
@@ -39,7 +53,7 @@ __global__ __launch_bounds__(kWave* kRowsPerBlock) void quantizeRows(
     std::int8_t* qr = q + std::size_t(row) * features;
     for (unsigned j = lane; j < features; j += kWave) {
         const int v = __float2int_rn(xr[j] / s);
-        qr[j] = std::int8_t(v < -127 ? -127 : (v > 127 ? 127 : v));
+        qr[Packed ? packedOffset(j) : j] = std::int8_t(v < -127 ? -127 : (v > 127 ? 127 : v));
     }
 }
 
@@ -57,6 +71,17 @@ __device__ __forceinline__ unsigned quantizeGroup(f32x4 v, float s) {
            (unsigned(quantizeOne(v.z, s)) & 0xFFu) << 16 | (unsigned(quantizeOne(v.w, s)) & 0xFFu) << 24;
 }
 
+// The packed16 dword of lane `lane` from the quantized dwords of its 16-feature tile, held by the
+// tile's four lanes (w0..w3 = features 0-3, 4-7, 8-11, 12-15): output dword i is bytes
+// [q(2i), q(2i+8), q(2i+1), q(2i+9)], i.e. two bytes of w(i/2) and two of w(i/2 + 2). All four lanes
+// of the tile must execute this together.
+__device__ __forceinline__ unsigned packDword(unsigned qd, unsigned lane) {
+    const unsigned lo = unsigned(__builtin_amdgcn_mov_dpp(int(qd), 0x50, 0xF, 0xF, false)); // quad [0,0,1,1]
+    const unsigned hi = unsigned(__builtin_amdgcn_mov_dpp(int(qd), 0xFA, 0xF, 0xF, false)); // quad [2,2,3,3]
+    // v_perm_b32 selectors: bytes 0-3 pick from the second operand, 4-7 from the first.
+    return __builtin_amdgcn_perm(hi, lo, (lane & 1u) ? 0x07030602u : 0x05010400u);
+}
+
 __device__ __forceinline__ float absMax(f32x4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
@@ -67,7 +92,7 @@ __device__ __forceinline__ float absMax(f32x4 v) {
 // X is streamed with nontemporal loads and q with nontemporal stores (neither is re-read here).
 constexpr unsigned kQuantRows = 4;
 
-template <unsigned Lanes>
+template <unsigned Lanes, bool Packed>
 __global__ __launch_bounds__(256) void quantizeRowsFit(const f32x4* __restrict__ x,
                                                         unsigned* __restrict__ q,
                                                         float* __restrict__ scale,
@@ -95,12 +120,15 @@ __global__ __launch_bounds__(256) void quantizeRowsFit(const f32x4* __restrict__
         if (row >= sources) break;
         const float s = m[r] == 0.0f ? 1.0f : m[r] / 127.0f;
         if (lane == 0) scale[row] = s;
-        if (lane < groups) __builtin_nontemporal_store(quantizeGroup(v[r], s), q + row * groups + lane);
+        unsigned qd = quantizeGroup(v[r], s);
+        if constexpr (Packed) qd = packDword(qd, lane); // the row's tiles are whole lane quads
+        if (lane < groups) __builtin_nontemporal_store(qd, q + row * groups + lane);
     }
 }
 
 // Rows of more than 64 groups: one wave per row, looping over the groups twice (maximum, then
 // quantize; the second read of the row hits L2).
+template <bool Packed>
 __global__ __launch_bounds__(256) void quantizeRowsLong(const f32x4* __restrict__ x,
                                                          unsigned* __restrict__ q,
                                                          float* __restrict__ scale,
@@ -116,7 +144,11 @@ __global__ __launch_bounds__(256) void quantizeRowsLong(const f32x4* __restrict_
     const float s = m == 0.0f ? 1.0f : m / 127.0f;
     if (lane == 0) scale[row] = s;
     unsigned* qr = q + row * groups;
-    for (unsigned j = lane; j < groups; j += kWave) qr[j] = quantizeGroup(xr[j], s);
+    for (unsigned j = lane; j < groups; j += kWave) {
+        unsigned qd = quantizeGroup(xr[j], s);
+        if constexpr (Packed) qd = packDword(qd, lane); // groups % 4 == 0: whole quads
+        qr[j] = qd;
+    }
 }
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -148,22 +180,24 @@ __global__ __launch_bounds__(256) void packPairs(const std::uint8_t* __restrict_
 
 } // namespace
 
-void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uint32_t sources,
-                          std::uint32_t features, hipStream_t stream) {
-    // A zero-sized grid is a launch error, reported like the runtime would (std::runtime_error).
-    if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
-    // A null buffer would fault the GPU; rejected before any launch (the reference does not check).
-    if (!x || !q || !scale) throw std::invalid_argument("quantize: null device buffer");
+namespace {
+
+// The quantize kernels for one call: the vector kernels for 16-byte aligned rows of features % 4 ==
+// 0 with a 4-byte aligned output, the scalar kernel otherwise. `Packed` writes the packed16 layout
+// (features % 16 == 0, checked by the caller).
+template <bool Packed>
+void launchQuantize(const float* x, std::int8_t* out, float* scale, std::uint32_t sources,
+                    std::uint32_t features, hipStream_t stream) {
     const bool vector = features % 4 == 0 && reinterpret_cast<std::uintptr_t>(x) % 16 == 0 &&
-                        reinterpret_cast<std::uintptr_t>(q) % 4 == 0;
+                        reinterpret_cast<std::uintptr_t>(out) % 4 == 0;
     if (vector) {
         const unsigned groups = features / 4;
         const auto* xv = reinterpret_cast<const f32x4*>(x);
-        auto* qv = reinterpret_cast<unsigned*>(q);
+        auto* qv = reinterpret_cast<unsigned*>(out);
         if (groups > kWave) {
             const unsigned blocks = unsigned((std::size_t(sources) * kWave + 255) / 256);
-            hipLaunchKernelGGL(quantizeRowsLong, dim3(blocks), dim3(256), 0, stream, xv, qv, scale,
-                               sources, groups);
+            hipLaunchKernelGGL(quantizeRowsLong<Packed>, dim3(blocks), dim3(256), 0, stream, xv, qv,
+                               scale, sources, groups);
         } else {
             unsigned lanes = 1;
             while (lanes < groups) lanes *= 2;
@@ -172,8 +206,8 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
             switch (lanes) {
 #define TCC_QUANT_CASE(L)                                                                          \
     case L:                                                                                        \
-        hipLaunchKernelGGL(quantizeRowsFit<L>, dim3(blocks), dim3(256), 0, stream, xv, qv, scale,  \
-                           sources, groups);                                                       \
+        hipLaunchKernelGGL((quantizeRowsFit<L, Packed>), dim3(blocks), dim3(256), 0, stream, xv,   \
+                           qv, scale, sources, groups);                                            \
         break;
                 TCC_QUANT_CASE(1) TCC_QUANT_CASE(2) TCC_QUANT_CASE(4) TCC_QUANT_CASE(8)
                 TCC_QUANT_CASE(16) TCC_QUANT_CASE(32) TCC_QUANT_CASE(64)
@@ -182,10 +216,29 @@ void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uin
         }
     } else {
         const unsigned blocks = unsigned((std::size_t(sources) + kRowsPerBlock - 1) / kRowsPerBlock);
-        hipLaunchKernelGGL(quantizeRows, dim3(blocks), dim3(kWave * kRowsPerBlock), 0, stream, x,
-                           q, scale, sources, features);
+        hipLaunchKernelGGL(quantizeRows<Packed>, dim3(blocks), dim3(kWave * kRowsPerBlock), 0,
+                           stream, x, out, scale, sources, features);
     }
     checkHip(hipGetLastError());
+}
+
+} // namespace
+
+void quantizeFeaturesInt8(const float* x, std::int8_t* q, float* scale, std::uint32_t sources,
+                          std::uint32_t features, hipStream_t stream) {
+    // A zero-sized grid is a launch error, reported like the runtime would (std::runtime_error).
+    if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
+    // A null buffer would fault the GPU; rejected before any launch (the reference does not check).
+    if (!x || !q || !scale) throw std::invalid_argument("quantize: null device buffer");
+    launchQuantize<false>(x, q, scale, sources, features, stream);
+}
+
+void quantizePackFeaturesInt8(const float* x, std::int8_t* packed, float* scale,
+                              std::uint32_t sources, std::uint32_t features, hipStream_t stream) {
+    if (!sources || !features) throw std::runtime_error("quantize: invalid configuration argument");
+    if (features % 16) throw std::invalid_argument("packed16 needs features % 16 == 0");
+    if (!x || !packed || !scale) throw std::invalid_argument("quantize-pack: null device buffer");
+    launchQuantize<true>(x, packed, scale, sources, features, stream);
 }
 
 void packFeaturesInt8x16(const std::int8_t* q, std::int8_t* packed, std::uint32_t sources,

@@ -91,6 +91,30 @@ def pack_features_int8x16(q: torch.Tensor, packed: torch.Tensor | None = None, s
     return packed
 
 
+def quantize_pack_features_int8(x: torch.Tensor, packed: torch.Tensor | None = None,
+                                scale: torch.Tensor | None = None, stream=None):
+    """quantizePackFeaturesInt8 (include/format/int8_features.h; no counterpart in the reference):
+    quantize_features_int8 then pack_features_int8x16 in one pass, bit-identical to that pair.
+
+    x: float32 [sources, features] on the GPU, features % 16 == 0. Returns (packed int8
+    [sources, features], scale f32)."""
+    if x.dtype != torch.float32 or x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 [sources, features] tensor")
+    sources, features = x.shape
+    if packed is not None:
+        _require_buffer(packed, "packed", torch.int8, sources * features)
+    if scale is not None:
+        _require_buffer(scale, "scale", torch.float32, sources)
+    _require_cuda(x, packed, scale)
+    _require_same_device(x.device, packed, scale)
+    packed = (torch.empty((sources, features), dtype=torch.int8, device=x.device)
+              if packed is None else packed)
+    scale = torch.empty(sources, dtype=torch.float32, device=x.device) if scale is None else scale
+    check(lib().tcc_quantize_pack_features_int8(_ptr(x), _ptr(packed), _ptr(scale), sources,
+                                                features, _stream_ptr(stream)))
+    return packed, scale
+
+
 def _check_operands(packed_x, scales, output, rows: int, cols: int, features: int,
                     workspace=None) -> None:
     """Layout and size first, then the device, so that every rejection happens before a launch.

@@ -131,6 +131,14 @@ def test_device_entry_points_reject_null_buffers_before_any_launch():
     for args in ((None, P), (P, None)):
         st = L.tcc_pack_features_int8x16(*args, 4, 128, None)
         assert st == 1 and b"null" in L.tcc_last_error()
+    for args in ((None, P, P), (P, None, P), (P, P, None)):
+        st = L.tcc_quantize_pack_features_int8(*args, 4, 128, None)
+        assert st == 1 and b"null" in L.tcc_last_error()
+    # the fused entry applies pack's width rule and quantize's size rule before anything else
+    st = L.tcc_quantize_pack_features_int8(P, P, P, 4, 24, None)
+    assert st == 1 and b"features % 16" in L.tcc_last_error()
+    st = L.tcc_quantize_pack_features_int8(P, P, P, 0, 128, None)
+    assert st == 3
 
 
 def test_noalloc_entry_point_rejects_before_any_launch():

@@ -489,6 +489,43 @@ def test_spmm_wide_addressing_at_real_size(oracle, gpu, feats):
     _check_full(ofmt, y, pk_u, sc_u, f"wide F{feats}")
 
 
+@pytest.mark.parametrize("shape,x_offset,out_offset", [
+    ((40, 64), 1, 0), ((9, 32), 0, 2), ((5, 16), 0, 1),    # scalar kernel: x or packed misaligned
+    ((3, 2048), 0, 0), ((70, 272), 0, 0),                   # long-row kernel: > 64 groups per row
+    ((1, 16), 0, 0), ((1029, 16), 0, 0), ((515, 48), 0, 0),  # fit kernel, 4 and 16 lanes (12 live)
+    ((257, 112), 0, 0), ((131, 128), 0, 0), ((67, 256), 0, 0),  # 32 and 64 lanes, ragged tail
+])
+def test_quantize_pack_fused_bit_exact(oracle, gpu, shape, x_offset, out_offset):
+    """quantizePackFeaturesInt8 writes exactly the scales and packed16 bytes of quantizeFeaturesInt8
+    followed by packFeaturesInt8x16, on every kernel path (scalar for misaligned x or output, long
+    rows, the register kernel with idle lanes and a partial last block), and the oracle's."""
+    import torch
+    from tcc_spmm_amd.device import quantize_pack_features_int8
+    s, f = shape
+    x = features(s, f, seed=s * 37 + f, stddev=2.0, outlier_fraction=0.1, outlier_scale=50.0)
+    x[0] = 0.0
+    flat = torch.zeros(s * f + x_offset, dtype=torch.float32, device=gpu)
+    flat[x_offset:] = torch.from_numpy(x.ravel()).to(gpu)
+    xs = flat[x_offset:].view(s, f)
+    out = torch.full((s * f + out_offset,), 0x5A, dtype=torch.int8, device=gpu)
+    packed, scale = quantize_pack_features_int8(xs, out[out_offset:].view(s, f))
+    torch.cuda.synchronize()
+    assert packed.data_ptr() % 4 == out_offset % 4
+    p2, s2, q2, sc2, pk2 = gpu_prepare(x, gpu)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), sc2.view(np.uint32))
+    assert np.array_equal(packed.cpu().numpy(), pk2)
+    q_ref, s_ref = oracle.quantize(x)
+    assert np.array_equal(packed.cpu().numpy(), oracle.pack16(q_ref))
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quantize_pack_fused_rejects_bad_widths(gpu):
+    import torch
+    from tcc_spmm_amd.device import quantize_pack_features_int8
+    with pytest.raises(ValueError, match="features % 16"):
+        quantize_pack_features_int8(torch.zeros((4, 24), dtype=torch.float32, device=gpu))
+
+
 @pytest.mark.parametrize("shape,offset", [
     ((33, 18), 0), ((20, 5), 0), ((40, 64), 1),            # scalar kernel: F % 4 != 0, misaligned
     ((3, 2052), 0), ((70, 260), 0),                         # long-row kernel: > 64 groups per row
