@@ -1,7 +1,8 @@
 // Fused INT8-dequantization SpMM for MI355X (gfx950, wave64): Y = A x tf32(dequant(X)).
 //
 // Work decomposition
-//   One workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW), normally one wavefront.
+//   One workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW), normally one wavefront;
+//   each XCD walks a contiguous range of the task list (xcdTask), balanced by panels when skewed.
 //   The wave walks the task's panels once, in order, and accumulates all 32 rows x F features of
 //   the SW: four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block;
 //   M = features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per
@@ -613,12 +614,57 @@ __device__ __forceinline__ void storeRow(const f32x16 (&acc)[4], float* rowBase,
     }
 }
 
-// Workgroup -> work item: each of the 8 XCDs (workgroups are dispatched round-robin by id) walks
-// one contiguous range of tasks, so neighbouring SWs share source rows of X in that XCD's L2.
-__device__ __forceinline__ unsigned xcdTask(unsigned bid, unsigned tasks) {
-    const unsigned xcd = bid & 7u, j = bid >> 3;
+// Workgroup -> task. Workgroups are dispatched to the 8 XCDs round-robin by id, and XCD x walks
+// one contiguous range of the task list, so neighbouring SWs share source rows of X in its L2. The
+// ranges hold equal task counts unless that leaves some XCD more than 3% above the mean panel
+// count (hub SWs cut into many 384-panel tasks); then the ranges hold equal panel counts, each
+// boundary moved at most kSpareShare / 2 of a share from its equal-count place. The grid carries
+// kSpareShare of a share of spare workgroups per XCD for the longer ranges; workgroups past their
+// XCD's range exit. Task begins never decrease along the list, so the panel-balanced boundaries
+// are binary searches, the same for every workgroup of an XCD.
+constexpr unsigned kSpareDiv = 16; // spare workgroups per XCD: ceil(T / 16), half a share
+
+__host__ __device__ inline unsigned spareWorkgroups(unsigned tasks) {
+    return (tasks + kSpareDiv - 1) / kSpareDiv;
+}
+
+__device__ __forceinline__ unsigned equalBound(unsigned tasks, unsigned x) {
     const unsigned q = tasks >> 3, r = tasks & 7u;
-    return xcd * q + min(xcd, r) + j;
+    return x * q + min(x, r);
+}
+
+// Returns false when the workgroup has no task.
+__device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsigned& task) {
+    const Sw32Task* tasks = a.m.tasks;
+    const unsigned count = a.m.taskCount, x = bid & 7u, j = bid >> 3;
+    auto beginOf = [&](unsigned t) { return t < count ? tasks[t].begin : tasks[count - 1].end; };
+    unsigned first[9];
+    unsigned maxPanels = 0;
+#pragma unroll
+    for (unsigned k = 0; k <= 8; ++k) first[k] = beginOf(equalBound(count, k));
+#pragma unroll
+    for (unsigned k = 0; k < 8; ++k) maxPanels = max(maxPanels, first[k + 1] - first[k]);
+    const std::uint64_t panels = first[8];
+    unsigned lo = equalBound(count, x), hi = equalBound(count, x + 1);
+    if (std::uint64_t(maxPanels) * 8 * 100 > panels * 103) {
+        const unsigned reach = spareWorkgroups(count) / 2;
+        auto bound = [&](unsigned k) -> unsigned {
+            if (k == 0 || k == 8) return equalBound(count, k);
+            const unsigned target = unsigned(panels * k / 8);
+            unsigned l = 0, h = count;
+            while (l < h) {
+                const unsigned mid = (l + h) >> 1;
+                if (tasks[mid].begin < target) l = mid + 1;
+                else h = mid;
+            }
+            const unsigned eq = equalBound(count, k);
+            return min(max(l, eq > reach ? eq - reach : 0u), eq + reach);
+        };
+        lo = bound(x);
+        hi = bound(x + 1);
+    }
+    task = lo + j;
+    return task < hi;
 }
 
 // One task over all S = Features / 128 slices of its SW, by `Waves` waves of one workgroup. With
@@ -754,7 +800,8 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
 template <unsigned Addr, unsigned Waves = 1>
 __global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 spmmInt8Kernel128(KernelArgs a) {
-    runTask<128, Addr, Waves>(a, xcdTask(blockIdx.x, a.m.taskCount));
+    unsigned task;
+    if (xcdTask(a, blockIdx.x, task)) runTask<128, Addr, Waves>(a, task);
 }
 
 // F256: both 128-feature slices of a task in one wave (128 accumulator registers, two waves per
@@ -764,7 +811,8 @@ spmmInt8Kernel128(KernelArgs a) {
 template <unsigned Addr, unsigned Waves = 1>
 __global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(2, 8))) void
 spmmInt8Kernel256(KernelArgs a) {
-    runTask<256, Addr, Waves>(a, xcdTask(blockIdx.x, a.m.taskCount));
+    unsigned task;
+    if (xcdTask(a, blockIdx.x, task)) runTask<256, Addr, Waves>(a, task);
 }
 
 // Waves per task: 2 when the plan has few tasks for the chip's wave slots, so that the longest
@@ -794,7 +842,7 @@ void launch(const KernelArgs& args, hipStream_t stream) {
     const bool misaligned = reinterpret_cast<std::uintptr_t>(args.packedX) % 16 != 0;
     const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull ||
                       std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
-    const dim3 grid(args.m.taskCount, 1);
+    const dim3 grid(args.m.taskCount + 8 * spareWorkgroups(args.m.taskCount), 1);
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kWave), 0, stream, args); };
     auto go2 = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(2 * kWave), 0, stream, args);
