@@ -3,7 +3,9 @@
  *
  * Replays the cache-line accesses of spmmInt8Kernel128/256 on one MI355X XCD through a
  * set-associative L2 and counts the misses of each stream. The kernel's schedule is modelled as it
- * runs: the task list is cut into 8 contiguous ranges, one per XCD (the kernel's xcdTask mapping);
+ * runs: the task list is cut into contiguous ranges, one per XCD, by the kernel's xcdTask rule
+ * (equal task counts unless an XCD would get more than 3% above the mean panel count, then equal
+ * panel counts with each boundary clamped to a quarter share from its equal-count place);
  * an XCD keeps `waves` tasks resident, gives them one panel each in turn, and starts the next task of
  * its range in a slot whose task has finished. One panel touches, in order:
  *   its sourceIds line, its sourceMetadata line, the values lines of its value range (A stream);
@@ -131,10 +133,44 @@ static int take_task(task_queue_t* tq, uint64_t* pos, uint64_t* end, uint32_t* s
     return 0;
 }
 
+/* Boundary k of the XCD ranges (xcdTask in spmm.hip, for any XCD count): equal task counts, or,
+ * when that leaves an XCD more than 3% above the mean panel count, the first task starting at or
+ * past k/xcds of the panels, clamped to half the spare share (ceil(T / (2 xcds)) workgroups per XCD)
+ * from its equal-count place. */
+static uint32_t equal_bound(uint32_t count, uint32_t xcds, uint32_t k) {
+    const uint32_t q = count / xcds, r = count % xcds;
+    return k * q + (k < r ? k : r);
+}
+
+static uint32_t task_begin(const l2m_input* in, uint32_t t) {
+    return t < in->taskCount ? in->tasks[(uint64_t)t * 7 + 1] : in->tasks[(uint64_t)(in->taskCount - 1) * 7 + 2];
+}
+
+static uint32_t xcd_bound(const l2m_input* in, uint32_t k) {
+    const uint32_t count = in->taskCount, xcds = in->xcds;
+    if (k == 0 || k >= xcds || count == 0) return equal_bound(count, xcds, k);
+    const uint64_t panels = task_begin(in, count);
+    uint64_t maxPanels = 0;
+    for (uint32_t j = 0; j < xcds; ++j) {
+        const uint64_t n = task_begin(in, equal_bound(count, xcds, j + 1)) - task_begin(in, equal_bound(count, xcds, j));
+        if (n > maxPanels) maxPanels = n;
+    }
+    const uint32_t eq = equal_bound(count, xcds, k);
+    if (maxPanels * xcds * 100 <= panels * 103) return eq;
+    const uint32_t target = (uint32_t)(panels * k / xcds);
+    uint32_t lo = 0, hi = count;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (task_begin(in, mid) < target) lo = mid + 1;
+        else hi = mid;
+    }
+    const uint32_t reach = ((count + 2 * xcds - 1) / (2 * xcds)) / 2;
+    const uint32_t floorB = eq > reach ? eq - reach : 0, ceilB = eq + reach;
+    return lo < floorB ? floorB : (lo > ceilB ? ceilB : lo);
+}
+
 static int build_sequence(const l2m_input* in, const layout_t* L, seq_t* s) {
-    const uint32_t q = in->taskCount / in->xcds, r = in->taskCount % in->xcds;
-    const uint32_t lo = in->xcd * q + (in->xcd < r ? in->xcd : r);
-    task_queue_t tq = {in, lo, lo + q + (in->xcd < r ? 1 : 0)};
+    task_queue_t tq = {in, xcd_bound(in, in->xcd), xcd_bound(in, in->xcd + 1)};
     const uint32_t W = in->waves ? in->waves : 1;
     uint64_t* pos = (uint64_t*)calloc(W, sizeof(uint64_t));
     uint64_t* end = (uint64_t*)calloc(W, sizeof(uint64_t));

@@ -14,18 +14,35 @@ def _format(cfg="t300_24_5"):
     return T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
 
 
+def _ranges(begins, total, xcds):
+    """The kernel's XCD ranges (xcdTask in spmm.hip), restated for any XCD count: equal task counts
+    unless an XCD would get more than 3% above the mean panel count; then each boundary is the first
+    task at or past k/xcds of the panels, clamped to half the spare share from its equal place."""
+    n = len(begins)
+    eq = [k * (n // xcds) + min(k, n % xcds) for k in range(xcds + 1)]
+    begin_of = lambda t: begins[t] if t < n else total
+    per = [begin_of(eq[k + 1]) - begin_of(eq[k]) for k in range(xcds)]
+    if max(per) * xcds * 100 <= total * 103:
+        return eq
+    reach = ((n + 2 * xcds - 1) // (2 * xcds)) // 2
+    out = [0]
+    for k in range(1, xcds):
+        lo = next((t for t in range(n) if begins[t] >= total * k // xcds), n)
+        out.append(min(max(lo, eq[k] - reach if eq[k] > reach else 0), eq[k] + reach))
+    return out + [n]
+
+
 def _sequence(fmt, features, xcd, xcds, waves):
-    """The model's access order, restated: contiguous task ranges per XCD, `waves` resident tasks
-    taking one panel each in turn; per panel the sourceIds, metadata and values lines, then per
-    real slot its X lines and scale line. Keys are (array, line)."""
+    """The model's access order, restated: the kernel's contiguous task range of this XCD, `waves`
+    resident tasks taking one panel each in turn; per panel the sourceIds, metadata and values
+    lines, then per real slot its X lines and scale line. Keys are (array, line)."""
     a = fmt.arrays(copy=False)
     tasks = [tuple(int(v) for v in t) for t in a["tasks"][["sw", "begin", "end"]]]
     ids = np.asarray(a["source_ids"])
     base = (np.asarray(a["source_metadata"])[::8] >> np.uint64(32)).astype(np.int64)
     n_panels, n_values = base.size, int(a["values"].size)
-    q, r = divmod(len(tasks), xcds)
-    lo = xcd * q + min(xcd, r)
-    queue = [t for t in tasks[lo:lo + q + (1 if xcd < r else 0)] if t[2] > t[1]]
+    b = _ranges([t[1] for t in tasks], tasks[-1][2], xcds)
+    queue = [t for t in tasks[b[xcd]:b[xcd + 1]] if t[2] > t[1]]
     slots = [None] * waves
     for w in range(waves):
         slots[w] = list(queue.pop(0)[1:]) if queue else None
@@ -106,6 +123,30 @@ def test_model_matches_an_independent_replay(policy, features):
     assert got["misses"] == want
 
 
+def test_ranges_follow_the_kernel_rule():
+    """t300_24_5's equal split is within 3% (kept); t2000_30_7's is not (balanced, boundaries moved)."""
+    for cfg, balanced in (("t300_24_5", False), ("t2000_30_7", True)):
+        tasks = _format(cfg).arrays(copy=False)["tasks"]
+        begins = [int(v) for v in tasks["begin"]]
+        n = len(begins)
+        b = _ranges(begins, int(tasks["end"][-1]), model.XCDS)
+        equal = [k * (n // 8) + min(k, n % 8) for k in range(9)]
+        assert b[0] == 0 and b[-1] == n and all(x <= y for x, y in zip(b, b[1:]))
+        assert (b != equal) == balanced, cfg
+
+
+def test_model_follows_balanced_ranges():
+    """The replay comparison on a format whose XCD ranges are panel-balanced (LRU only)."""
+    fmt = _format("t2000_30_7")
+    lines, waves = 64, 6
+    got = model.traffic(fmt, 128, "lru", waves=waves, l2_bytes=lines * LINE, ways=lines)
+    want = {s: 0 for s in model.STREAMS}
+    for xcd in range(model.XCDS):
+        for st, n in _replay(_sequence(fmt, 128, xcd, model.XCDS, waves), lines, "lru").items():
+            want[st] += n
+    assert got["misses"] == want
+
+
 def test_policies_are_ordered_and_bytes_add_up():
     fmt = _format("t2000_30_7")
     r = {p: model.traffic(fmt, 128, p) for p in ("cold", "opt", "lru")}
@@ -124,11 +165,10 @@ def test_cold_misses_are_distinct_lines_per_xcd():
     fmt = _format("t2000_30_7")
     a = fmt.arrays(copy=False)
     tasks, ids = a["tasks"], np.asarray(a["source_ids"])
-    q, r = divmod(len(tasks), model.XCDS)
+    b = _ranges([int(v) for v in tasks["begin"]], int(tasks["end"][-1]), model.XCDS)
     want = 0
     for x in range(model.XCDS):
-        lo = x * q + min(x, r)
-        part = tasks[lo:lo + q + (1 if x < r else 0)]
+        part = tasks[b[x]:b[x + 1]]
         if not len(part):
             continue
         src = ids[int(part["begin"][0]) * 8:int(part["end"][-1]) * 8]
