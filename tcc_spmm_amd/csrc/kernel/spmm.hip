@@ -618,10 +618,10 @@ __device__ __forceinline__ void storeRow(const f32x16 (&acc)[4], float* rowBase,
 // one contiguous range of the task list, so neighbouring SWs share source rows of X in its L2. The
 // ranges hold equal task counts unless that leaves some XCD more than 3% above the mean panel
 // count (hub SWs cut into many 384-panel tasks); then the ranges hold equal panel counts, each
-// boundary moved at most kSpareShare / 2 of a share from its equal-count place. The grid carries
-// kSpareShare of a share of spare workgroups per XCD for the longer ranges; workgroups past their
-// XCD's range exit. Task begins never decrease along the list, so the panel-balanced boundaries
-// are binary searches, the same for every workgroup of an XCD.
+// boundary moved at most a quarter of a share (T / 32 tasks) from its equal-count place. The grid
+// carries half a share (ceil(T / 16)) of spare workgroups per XCD, enough for the longest range
+// this allows; workgroups past their XCD's range exit. Task begins never decrease along the list,
+// so the panel-balanced boundaries are binary searches, the same for every workgroup of an XCD.
 constexpr unsigned kSpareDiv = 16; // spare workgroups per XCD: ceil(T / 16), half a share
 
 __host__ __device__ inline unsigned spareWorkgroups(unsigned tasks) {
