@@ -58,7 +58,7 @@ PROBE = HERE / "_build" / "gather_probe"
 
 
 def _lib():
-    if not SO.exists():
+    if not SO.exists() or SO.stat().st_mtime < (HERE / "l2_model.c").stat().st_mtime:
         build()
     so = C.CDLL(str(SO))
     so.l2m_replay.argtypes = [C.POINTER(_Input), C.POINTER(_Result)]

@@ -7,7 +7,8 @@
  * (equal task counts unless an XCD would get more than 3% above the mean panel count, then equal
  * panel counts with each boundary clamped to a quarter share from its equal-count place);
  * an XCD keeps `waves` tasks resident, gives them one panel each in turn, and starts the next task of
- * its range in a slot whose task has finished. One panel touches, in order:
+ * its range in a slot whose task has finished, the last 512 tasks of the range longest size class
+ * first. One panel touches, in order:
  *   its sourceIds line, its sourceMetadata line, the values lines of its value range (A stream);
  *   then per slot (padding slots excluded) the F/128 lines of the source's packed X row and the
  *   line of its 4-byte scale.
@@ -112,16 +113,41 @@ static int panel_accesses(const l2m_input* in, const layout_t* L, uint64_t p, ui
     return 0;
 }
 
-/* The XCD's task range, scheduled as the kernel runs it. */
+/* The XCD's task range in the kernel's dispatch order: list order, except that the last TAIL_WINDOW
+ * tasks of the range run longest size class first (panel counts >= 288, >= 192, >= 96, the rest;
+ * list order within a class). */
+enum { TAIL_WINDOW = 512 };
+
 typedef struct {
     const l2m_input* in;
-    uint32_t next, hi;
+    uint32_t next, hi, w0;
+    uint32_t window[TAIL_WINDOW];
 } task_queue_t;
+
+static uint32_t size_class(const l2m_input* in, uint32_t t) {
+    const uint32_t* r = in->tasks + (uint64_t)t * 7;
+    const uint32_t p = r[2] - r[1];
+    return (uint32_t)(p >= 96) + (uint32_t)(p >= 192) + (uint32_t)(p >= 288);
+}
+
+static void queue_init(task_queue_t* tq, const l2m_input* in, uint32_t lo, uint32_t hi) {
+    const uint32_t n = hi - lo < TAIL_WINDOW ? hi - lo : TAIL_WINDOW;
+    tq->in = in;
+    tq->next = lo;
+    tq->hi = hi;
+    tq->w0 = hi - n;
+    uint32_t k = 0;
+    for (int c = 3; c >= 0; --c)
+        for (uint32_t t = tq->w0; t < hi; ++t)
+            if (size_class(in, t) == (uint32_t)c) tq->window[k++] = t;
+}
 
 /* Gives slot w the next task with at least one panel; returns 0 when the range is exhausted. */
 static int take_task(task_queue_t* tq, uint64_t* pos, uint64_t* end, uint32_t* sw) {
     while (tq->next < tq->hi) {
-        const uint32_t* t = tq->in->tasks + (uint64_t)tq->next++ * 7;
+        const uint32_t i = tq->next++;
+        const uint32_t task = i >= tq->w0 ? tq->window[i - tq->w0] : i;
+        const uint32_t* t = tq->in->tasks + (uint64_t)task * 7;
         if (t[2] > t[1]) {
             *pos = t[1];
             *end = t[2];
@@ -170,7 +196,8 @@ static uint32_t xcd_bound(const l2m_input* in, uint32_t k) {
 }
 
 static int build_sequence(const l2m_input* in, const layout_t* L, seq_t* s) {
-    task_queue_t tq = {in, xcd_bound(in, in->xcd), xcd_bound(in, in->xcd + 1)};
+    task_queue_t tq;
+    queue_init(&tq, in, xcd_bound(in, in->xcd), xcd_bound(in, in->xcd + 1));
     const uint32_t W = in->waves ? in->waves : 1;
     uint64_t* pos = (uint64_t*)calloc(W, sizeof(uint64_t));
     uint64_t* end = (uint64_t*)calloc(W, sizeof(uint64_t));

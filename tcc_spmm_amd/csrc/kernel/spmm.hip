@@ -2,7 +2,8 @@
 //
 // Work decomposition
 //   One workgroup per task (one Sw32Task: <= 384 panels of one 32-row SW), normally one wavefront;
-//   each XCD walks a contiguous range of the task list (xcdTask), balanced by panels when skewed.
+//   each XCD walks a contiguous range of the task list (xcdTask), balanced by panels when skewed,
+//   the range's last 512 tasks longest size class first (tailTask).
 //   The wave walks the task's panels once, in order, and accumulates all 32 rows x F features of
 //   the SW: four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block;
 //   M = features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per
@@ -633,6 +634,52 @@ __device__ __forceinline__ unsigned equalBound(unsigned tasks, unsigned x) {
     return x * q + min(x, r);
 }
 
+// The tail window: the last kTailWindow tasks of an XCD's range run longest size class first
+// (panels >= 288, >= 192, >= 96, the rest; list order within a class), so that the launch does not
+// end on a few long tasks started last. The window spans about the SWs an XCD holds resident at its
+// end anyway, so the order inside it leaves the L2 sharing of the in-order walk in place.
+constexpr unsigned kTailWindow = 512;
+
+__device__ __forceinline__ unsigned sizeClass(const Sw32Task* tasks, unsigned t) {
+    const unsigned p = tasks[t].end - tasks[t].begin;
+    return unsigned(p >= 96) + unsigned(p >= 192) + unsigned(p >= 288);
+}
+
+// Task at position r (r < n) of the window [w0, w0 + n) in size-class order. One wave, all lanes
+// active; every wave computes the same permutation of the window.
+__device__ __forceinline__ unsigned tailTask(const Sw32Task* tasks, unsigned w0, unsigned n,
+                                             unsigned r, unsigned lane) {
+    unsigned counts[4] = {0, 0, 0, 0};
+#pragma unroll 1
+    for (unsigned base = 0; base < n; base += kWave) {
+        const unsigned i = base + lane;
+        const unsigned cls = i < n ? sizeClass(tasks, w0 + i) : 4u;
+#pragma unroll
+        for (unsigned c = 0; c < 4; ++c)
+            counts[c] += unsigned(__builtin_popcountll(__builtin_amdgcn_ballot_w64(cls == c)));
+    }
+    unsigned c = 3, k = r;
+    while (c > 0 && k >= counts[c]) {
+        k -= counts[c];
+        --c;
+    }
+#pragma unroll 1
+    for (unsigned base = 0; base < n; base += kWave) {
+        const unsigned i = base + lane;
+        const bool member = i < n && sizeClass(tasks, w0 + i) == c;
+        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(member);
+        const unsigned count = unsigned(__builtin_popcountll(mask));
+        if (k < count) {
+            const unsigned below = __builtin_amdgcn_mbcnt_hi(unsigned(mask >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(unsigned(mask), 0u));
+            const std::uint64_t hit = __builtin_amdgcn_ballot_w64(member && below == k);
+            return w0 + base + unsigned(__builtin_ctzll(hit));
+        }
+        k -= count;
+    }
+    return w0 + r; // not reached: the window holds n tasks
+}
+
 // Returns false when the workgroup has no task.
 __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsigned& task) {
     const Sw32Task* tasks = a.m.tasks;
@@ -664,7 +711,10 @@ __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsig
         hi = bound(x + 1);
     }
     task = lo + j;
-    return task < hi;
+    if (task >= hi) return false;
+    const unsigned n = min(hi - lo, kTailWindow), w0 = hi - n;
+    if (task >= w0) task = tailTask(tasks, w0, n, task - w0, threadIdx.x & (kWave - 1));
+    return true;
 }
 
 // One task over all S = Features / 128 slices of its SW, by `Waves` waves of one workgroup. With

@@ -7,6 +7,7 @@ import model
 import tcc_spmm_amd as T
 
 LINE = 128
+TAIL_WINDOW = 512
 
 
 def _format(cfg="t300_24_5"):
@@ -33,8 +34,9 @@ def _ranges(begins, total, xcds):
 
 
 def _sequence(fmt, features, xcd, xcds, waves):
-    """The model's access order, restated: the kernel's contiguous task range of this XCD, `waves`
-    resident tasks taking one panel each in turn; per panel the sourceIds, metadata and values
+    """The model's access order, restated: the kernel's contiguous task range of this XCD (its last
+    TAIL_WINDOW tasks longest size class first, a stable sort), `waves` resident tasks taking one
+    panel each in turn; per panel the sourceIds, metadata and values
     lines, then per real slot its X lines and scale line. Keys are (array, line)."""
     a = fmt.arrays(copy=False)
     tasks = [tuple(int(v) for v in t) for t in a["tasks"][["sw", "begin", "end"]]]
@@ -42,7 +44,11 @@ def _sequence(fmt, features, xcd, xcds, waves):
     base = (np.asarray(a["source_metadata"])[::8] >> np.uint64(32)).astype(np.int64)
     n_panels, n_values = base.size, int(a["values"].size)
     b = _ranges([t[1] for t in tasks], tasks[-1][2], xcds)
-    queue = [t for t in tasks[b[xcd]:b[xcd + 1]] if t[2] > t[1]]
+    lo, hi = b[xcd], b[xcd + 1]
+    w0 = hi - min(hi - lo, TAIL_WINDOW)
+    size_class = lambda t: sum(t[2] - t[1] >= v for v in (96, 192, 288))
+    order = list(range(lo, w0)) + sorted(range(w0, hi), key=lambda i: -size_class(tasks[i]))
+    queue = [tasks[i] for i in order if tasks[i][2] > tasks[i][1]]
     slots = [None] * waves
     for w in range(waves):
         slots[w] = list(queue.pop(0)[1:]) if queue else None
@@ -145,6 +151,43 @@ def test_model_follows_balanced_ranges():
         for st, n in _replay(_sequence(fmt, 128, xcd, model.XCDS, waves), lines, "lru").items():
             want[st] += n
     assert got["misses"] == want
+
+
+def _mixed_format():
+    """48 SWs whose tasks fall in every size class (panel counts from 8 to about 340), in an
+    order where the tail window's class order differs from list order."""
+    rng = np.random.default_rng(3)
+    sws, cols = 48, 6000
+    degree = rng.choice([2, 40, 75, 110], sws)
+    offsets, ids = [0], []
+    for s in range(sws):
+        for _ in range(32):
+            ids.extend(np.sort(rng.choice(cols, degree[s], replace=False)))
+            offsets.append(len(ids))
+    ids = np.asarray(ids, np.uint32)
+    csr = T.csr_from_arrays(sws * 32, cols, np.asarray(offsets, np.uint32), ids,
+                            np.ones(ids.size, np.float32))
+    return T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+
+
+def test_model_follows_the_tail_order():
+    """The replay comparison on a format whose ranges lie inside the tail window and mix size
+    classes, so the dispatch order is not list order (LRU only)."""
+    fmt = _mixed_format()
+    tasks = fmt.arrays(copy=False)["tasks"]
+    p = (tasks["end"] - tasks["begin"]).astype(np.int64)
+    classes = (p >= 96).astype(int) + (p >= 192) + (p >= 288)
+    assert np.bincount(classes, minlength=4).min() > 0
+    assert any(np.any(np.diff(classes[b:e]) > 0) for b, e in zip(range(0, 48, 6), range(6, 54, 6)))
+    lines, waves = 64, 3
+    for features in (128, 256):
+        got = model.traffic(fmt, features, "lru", waves=waves, l2_bytes=lines * LINE, ways=lines)
+        want = {s: 0 for s in model.STREAMS}
+        for xcd in range(model.XCDS):
+            for st, n in _replay(_sequence(fmt, features, xcd, model.XCDS, waves), lines,
+                                 "lru").items():
+                want[st] += n
+        assert got["misses"] == want, features
 
 
 def test_policies_are_ordered_and_bytes_add_up():

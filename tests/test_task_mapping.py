@@ -4,13 +4,48 @@ every task exactly once for any task list.
 Workgroups are dispatched to the 8 XCDs round-robin; XCD x walks one contiguous range of tasks. The
 ranges hold equal task counts unless some XCD would get more than 3% above the mean panel count;
 then they hold equal panel counts, each boundary clamped to half the spare share from its equal-count
-place, and the grid adds ceil(T / 16) spare workgroups per XCD. Checked on the synthetic configs and
-on adversarial lists (all tasks empty, one task holding every panel, heavy skew, random sizes), for
-task counts 1..39 and a few larger ones."""
+place, and the grid adds ceil(T / 16) spare workgroups per XCD. The last TAIL_WINDOW tasks of a
+range run longest size class first (tailTask: per 64-lane chunk a ballot count of each class, then
+the k-th member of the chosen class by its rank among the chunk's members). Checked on the synthetic
+configs and on adversarial lists (all tasks empty, one task holding every panel, heavy skew, random
+sizes), for task counts 1..39 and a few larger ones; the window's order is checked against a stable
+sort by descending class."""
 import numpy as np
 import pytest
 
 import tcc_spmm_amd as T
+
+
+TAIL_WINDOW = 512
+WAVE = 64
+
+
+def _size_class(panels):
+    return (panels >= 96).astype(np.int64) + (panels >= 192) + (panels >= 288)
+
+
+def _tail_order(cls, w0):
+    """tailTask for every position r of the window [w0, w0 + cls.size); cls holds its classes."""
+    chunks = [cls[base:base + WAVE] for base in range(0, cls.size, WAVE)]
+    counts = [sum(int(np.count_nonzero(ch == c)) for ch in chunks) for c in range(4)]
+    # Per chunk and class, the member lanes by rank: the lane whose mbcnt (members in lower lanes)
+    # equals k is the k-th member.
+    lanes = [[np.flatnonzero(ch == c) for c in range(4)] for ch in chunks]
+    order = []
+    for r in range(cls.size):
+        c, k = 3, r
+        while c > 0 and k >= counts[c]:
+            k -= counts[c]
+            c -= 1
+        for i, per_class in enumerate(lanes):
+            member = per_class[c]
+            if k < member.size:
+                order.append(w0 + i * WAVE + int(member[k]))
+                break
+            k -= member.size
+        else:
+            raise AssertionError("the window holds every position")
+    return order
 
 
 def _spare(count):
@@ -42,12 +77,21 @@ def _bounds(begin, panels_total):
 def _covered_once(begin, panels_total):
     count = len(begin)
     balanced, b = _bounds(begin, panels_total)
+    cls = _size_class(np.diff(np.append(begin, panels_total)))
+    windows = {}
+    for x in range(8):
+        lo, hi = b[x], b[x + 1]
+        w0 = hi - min(hi - lo, TAIL_WINDOW)
+        order = _tail_order(cls[w0:hi], w0)
+        assert order == [w0 + i for i in np.argsort(-cls[w0:hi], kind="stable")]
+        windows[x] = (w0, order)
     seen = np.zeros(count, np.int64)
     for bid in range(count + 8 * _spare(count)):
         x, j = bid & 7, bid >> 3
         t = b[x] + j
         if t < b[x + 1]:
-            seen[t] += 1
+            w0, order = windows[x]
+            seen[order[t - w0] if t >= w0 else t] += 1
     return balanced, bool((seen == 1).all())
 
 
