@@ -645,45 +645,76 @@ __device__ __forceinline__ unsigned sizeClass(const Sw32Task* tasks, unsigned t)
     return unsigned(p >= 96) + unsigned(p >= 192) + unsigned(p >= 288);
 }
 
-// Task at position r (r < n) of the window [w0, w0 + n) in size-class order. One wave, all lanes
-// active; every wave computes the same permutation of the window.
+// Task at position r (r < n <= kTailWindow) of the window [w0, w0 + n) in size-class order. One
+// wave, all lanes active; every wave computes the same permutation of the window. The classes of
+// the window's tasks are loaded once (lane L: tasks L, L + 64, ...; all loads in flight together),
+// kept two bits per task in registers, and both passes below work on those.
 __device__ __forceinline__ unsigned tailTask(const Sw32Task* tasks, unsigned w0, unsigned n,
                                              unsigned r, unsigned lane) {
+    constexpr unsigned kChunks = kTailWindow / kWave, kWords = (kChunks + 15) / 16;
+    unsigned bits[kWords] = {};
+#pragma unroll
+    for (unsigned ch = 0; ch < kChunks; ++ch)
+        bits[ch / 16] |= sizeClass(tasks, w0 + min(ch * kWave + lane, n - 1)) << (2 * (ch % 16));
+    auto member = [&](unsigned ch, unsigned c) {
+        return ch * kWave + lane < n && ((bits[ch / 16] >> (2 * (ch % 16))) & 3u) == c;
+    };
     unsigned counts[4] = {0, 0, 0, 0};
-#pragma unroll 1
-    for (unsigned base = 0; base < n; base += kWave) {
-        const unsigned i = base + lane;
-        const unsigned cls = i < n ? sizeClass(tasks, w0 + i) : 4u;
+#pragma unroll
+    for (unsigned ch = 0; ch < kChunks; ++ch)
 #pragma unroll
         for (unsigned c = 0; c < 4; ++c)
-            counts[c] += unsigned(__builtin_popcountll(__builtin_amdgcn_ballot_w64(cls == c)));
-    }
+            counts[c] += unsigned(__builtin_popcountll(__builtin_amdgcn_ballot_w64(member(ch, c))));
     unsigned c = 3, k = r;
     while (c > 0 && k >= counts[c]) {
         k -= counts[c];
         --c;
     }
-#pragma unroll 1
-    for (unsigned base = 0; base < n; base += kWave) {
-        const unsigned i = base + lane;
-        const bool member = i < n && sizeClass(tasks, w0 + i) == c;
-        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(member);
+#pragma unroll
+    for (unsigned ch = 0; ch < kChunks; ++ch) {
+        const bool in = member(ch, c);
+        const std::uint64_t mask = __builtin_amdgcn_ballot_w64(in);
         const unsigned count = unsigned(__builtin_popcountll(mask));
         if (k < count) {
             const unsigned below = __builtin_amdgcn_mbcnt_hi(unsigned(mask >> 32),
                                                              __builtin_amdgcn_mbcnt_lo(unsigned(mask), 0u));
-            const std::uint64_t hit = __builtin_amdgcn_ballot_w64(member && below == k);
-            return w0 + base + unsigned(__builtin_ctzll(hit));
+            const std::uint64_t hit = __builtin_amdgcn_ballot_w64(in && below == k);
+            return w0 + ch * kWave + unsigned(__builtin_ctzll(hit));
         }
         k -= count;
     }
     return w0 + r; // not reached: the window holds n tasks
 }
 
+// Boundaries x and x + 1 of the panel-balanced ranges: the first task starting at or past k/8 of
+// the panels (k = x, x + 1; `count` when none does). Lanes 32h .. 32h + 31 search boundary x + h
+// together: each step probes 32 evenly spaced tasks of the half's interval [l, r] (task r is known
+// to qualify; r = count stands for past the end) and keeps the stretch between the last probe
+// below the target and the first one at or past it, so a search takes about log32(T) dependent
+// loads instead of log2(T). Returns the boundary of each lane's half.
+__device__ __forceinline__ unsigned panelBound(const Sw32Task* tasks, unsigned count,
+                                               std::uint64_t panels, unsigned x, unsigned lane) {
+    const unsigned h = lane >> 5, j = lane & 31;
+    const unsigned target = unsigned(panels * (x + h) / 8);
+    unsigned l = 0, r = count;
+    while (__builtin_amdgcn_ballot_w64(l < r) != 0) {
+        const unsigned stride = (r - l + 31) / 32; // 32 probes cover [l, r): r - l <= 32 stride
+        const unsigned q = l + j * stride;
+        const bool at = q >= r || tasks[min(q, count - 1)].begin >= target;
+        const unsigned half = unsigned(__builtin_amdgcn_ballot_w64(at) >> (32 * h));
+        const unsigned first = half ? unsigned(__builtin_ctz(half)) : 32u;
+        const unsigned nl = first == 0 ? l : l + (first - 1) * stride + 1;
+        r = first < 32 ? min(l + first * stride, r) : r;
+        l = nl;
+    }
+    return l;
+}
+
 // Returns false when the workgroup has no task.
 __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsigned& task) {
     const Sw32Task* tasks = a.m.tasks;
     const unsigned count = a.m.taskCount, x = bid & 7u, j = bid >> 3;
+    const unsigned lane = threadIdx.x & (kWave - 1);
     auto beginOf = [&](unsigned t) { return t < count ? tasks[t].begin : tasks[count - 1].end; };
     unsigned first[9];
     unsigned maxPanels = 0;
@@ -695,25 +726,16 @@ __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsig
     unsigned lo = equalBound(count, x), hi = equalBound(count, x + 1);
     if (std::uint64_t(maxPanels) * 8 * 100 > panels * 103) {
         const unsigned reach = spareWorkgroups(count) / 2;
-        auto bound = [&](unsigned k) -> unsigned {
-            if (k == 0 || k == 8) return equalBound(count, k);
-            const unsigned target = unsigned(panels * k / 8);
-            unsigned l = 0, h = count;
-            while (l < h) {
-                const unsigned mid = (l + h) >> 1;
-                if (tasks[mid].begin < target) l = mid + 1;
-                else h = mid;
-            }
-            const unsigned eq = equalBound(count, k);
-            return min(max(l, eq > reach ? eq - reach : 0u), eq + reach);
-        };
-        lo = bound(x);
-        hi = bound(x + 1);
+        const unsigned searched = panelBound(tasks, count, panels, x, lane);
+        const unsigned k = x + (lane >> 5), eq = equalBound(count, k);
+        const unsigned b = (k == 0 || k == 8) ? eq : min(max(searched, eq > reach ? eq - reach : 0u), eq + reach);
+        lo = __builtin_amdgcn_readlane(b, 0);
+        hi = __builtin_amdgcn_readlane(b, 32);
     }
     task = lo + j;
     if (task >= hi) return false;
     const unsigned n = min(hi - lo, kTailWindow), w0 = hi - n;
-    if (task >= w0) task = tailTask(tasks, w0, n, task - w0, threadIdx.x & (kWave - 1));
+    if (task >= w0) task = tailTask(tasks, w0, n, task - w0, lane);
     return true;
 }
 
@@ -818,28 +840,55 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     for (unsigned k = 0; k < S; ++k) {
         if (!lastFlag[k]) continue;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // Merge the slice: each lane sums columns lane and lane + 64, adding the partial tiles in
-        // partialIds (task) order starting from 0.0f.
-        const unsigned mcol = k * kSlice + lane;
+        // Merge the slice, one row group (8 rows x 128 columns) at a time: lane L sums the four
+        // 16-byte column blocks (L & 7) + 8j, j < 4, of row L >> 3, adding the partial tiles in
+        // partialIds (task) order starting from 0.0f. The group's tile ids are loaded once (one per
+        // lane, broadcast by readlane), and the loads of four tiles are issued before they are
+        // added, so a merge of many chunks waits for one load latency per four tiles, not per tile.
+        constexpr unsigned kMergeBatch = 2;
+        const unsigned mrow = lane >> 3, mcol = k * kSlice + (lane & 7) * 4;
 #pragma unroll 1
         for (unsigned g = 0; g < 4; ++g) {
             const Sw32ReduceRange red = a.m.reductions[task.reduceFirst + g];
             const unsigned row0 = sw * 32 + g * 8;
             if (row0 >= a.rows) continue;
-            const unsigned valid = min(8u, a.rows - row0);
+            f32x4 sum[4];
+#pragma unroll
+            for (unsigned j = 0; j < 4; ++j) sum[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            auto tileRow = [&](unsigned id) {
+                return reinterpret_cast<const f32x4*>(a.partials + (std::size_t(id) * 8 + mrow) * Features +
+                                                      mcol);
+            };
 #pragma unroll 1
-            for (unsigned r = 0; r < valid; ++r) {
-                float lo = 0.0f, hi = 0.0f;
+            for (unsigned base = red.begin; base < red.end; base += kWave) {
+                const unsigned items = min(red.end - base, kWave);
+                const unsigned ids = a.m.partialIds[base + min(lane, items - 1)];
+                unsigned i = 0;
 #pragma unroll 1
-                for (unsigned item = red.begin; item < red.end; ++item) {
-                    const float* pr =
-                        a.partials + (std::size_t(a.m.partialIds[item]) * 8 + r) * Features + mcol;
-                    lo += pr[0];
-                    hi += pr[kWave];
+                for (; i + kMergeBatch <= items; i += kMergeBatch) {
+                    f32x4 v[kMergeBatch][4];
+#pragma unroll
+                    for (unsigned u = 0; u < kMergeBatch; ++u) {
+                        const f32x4* src = tileRow(__builtin_amdgcn_readlane(ids, i + u));
+#pragma unroll
+                        for (unsigned j = 0; j < 4; ++j) v[u][j] = src[8 * j];
+                    }
+#pragma unroll
+                    for (unsigned u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+                        for (unsigned j = 0; j < 4; ++j) sum[j] += v[u][j];
                 }
-                float* yr = a.y + std::size_t(row0 + r) * Features + mcol;
-                yr[0] = lo;
-                yr[kWave] = hi;
+#pragma unroll 1
+                for (; i < items; ++i) {
+                    const f32x4* src = tileRow(__builtin_amdgcn_readlane(ids, i));
+#pragma unroll
+                    for (unsigned j = 0; j < 4; ++j) sum[j] += src[8 * j];
+                }
+            }
+            if (row0 + mrow < a.rows) {
+                f32x4* yr = reinterpret_cast<f32x4*>(a.y + std::size_t(row0 + mrow) * Features + mcol);
+#pragma unroll
+                for (unsigned j = 0; j < 4; ++j) yr[8 * j] = sum[j];
             }
         }
     }

@@ -48,6 +48,20 @@ def _tail_order(cls, w0):
     return order
 
 
+def _panel_bound(begin, count, target):
+    """panelBound for one half: 32 probes per step over [l, r], task r known to qualify."""
+    l, r = 0, count
+    while l < r:
+        stride = (r - l + 31) // 32
+        at = [l + j * stride >= r or begin[min(l + j * stride, count - 1)] >= target
+              for j in range(32)]
+        first = at.index(True) if True in at else 32
+        nl = l if first == 0 else l + (first - 1) * stride + 1
+        r = min(l + first * stride, r) if first < 32 else r
+        l = nl
+    return l
+
+
 def _spare(count):
     return (count + 15) // 16
 
@@ -119,3 +133,25 @@ def test_adversarial_lists():
                 sizes = np.where(rng.random(n) < 0.05, 384, rng.integers(0, 3, n))
             begin = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
             assert _covered_once(begin, int(sizes.sum()))[1], (kind, n)
+
+
+def test_probe_search_is_a_lower_bound():
+    """The kernel's 32-probe boundary search finds the first task at or past the target, as a
+    binary search does: non-decreasing begins with runs of equal values (empty tasks), targets
+    before, between, on and past the begins."""
+    rng = np.random.default_rng(5)
+    for n in list(range(1, 70)) + [1000, 38281, 79199]:
+        for kind in ("random", "runs", "empty"):
+            if kind == "random":
+                sizes = rng.integers(0, 385, n)
+            elif kind == "runs":
+                sizes = np.where(rng.random(n) < 0.7, 0, rng.integers(1, 385, n))
+            else:
+                sizes = np.zeros(n, np.int64)
+            begin = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+            total = int(sizes.sum())
+            targets = {0, total, total + 1} | {total * k // 8 for k in range(9)}
+            targets |= set(int(v) for v in rng.integers(0, total + 2, 8))
+            for target in targets:
+                want = int(np.searchsorted(begin, target, side="left"))
+                assert _panel_bound(begin, n, target) == want, (kind, n, target)
