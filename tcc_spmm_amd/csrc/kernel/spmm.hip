@@ -37,7 +37,7 @@
 //
 // The panels are walked by a software pipeline (metadata two panels ahead, in pairs of panels at
 // F128; A values and X one panel ahead) whose memory operations are identical on every path. F128
-// runs four waves per SIMD (128 registers each, accumulators included), F256 two (192 registers).
+// runs four waves per SIMD (128 registers each, accumulators included), F256 two (196 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes, per slice, an agent-scope
@@ -622,7 +622,8 @@ __device__ __forceinline__ void storeRow(const f32x16 (&acc)[4], float* rowBase,
 // boundary moved at most a quarter of a share (T / 32 tasks) from its equal-count place. The grid
 // carries half a share (ceil(T / 16)) of spare workgroups per XCD, enough for the longest range
 // this allows; workgroups past their XCD's range exit. Task begins never decrease along the list,
-// so the panel-balanced boundaries are binary searches, the same for every workgroup of an XCD.
+// so the panel-balanced boundaries are searches over them (panelBound), the same for every
+// workgroup of an XCD.
 constexpr unsigned kSpareDiv = 16; // spare workgroups per XCD: ceil(T / 16), half a share
 
 __host__ __device__ inline unsigned spareWorkgroups(unsigned tasks) {
