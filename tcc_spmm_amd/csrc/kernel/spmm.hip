@@ -844,8 +844,9 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
         // Merge the slice, one row group (8 rows x 128 columns) at a time: lane L sums the four
         // 16-byte column blocks (L & 7) + 8j, j < 4, of row L >> 3, adding the partial tiles in
         // partialIds (task) order starting from 0.0f. The group's tile ids are loaded once (one per
-        // lane, broadcast by readlane), and the loads of four tiles are issued before they are
-        // added, so a merge of many chunks waits for one load latency per four tiles, not per tile.
+        // lane, broadcast by readlane), and the loads of kMergeBatch tiles are issued before they
+        // are added, so a merge of many chunks waits for one load latency per batch, not per tile.
+        // More than two tiles in flight spill at F128.
         constexpr unsigned kMergeBatch = 2;
         const unsigned mrow = lane >> 3, mcol = k * kSlice + (lane & 7) * 4;
 #pragma unroll 1
