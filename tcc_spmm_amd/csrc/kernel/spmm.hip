@@ -93,6 +93,9 @@ struct KernelArgs {
     float* partials;
     unsigned* counters;
     unsigned rows, cols;
+#ifdef TCC_SPMM_TIMELINE
+    unsigned long long* stamps; // measurement build only: [taskCount][4], see TaskClock
+#endif
 };
 
 // sw32BucketOrder (include/format/sw32.h) packed four bits per bucket slot: slot t's row-group mask
@@ -896,13 +899,43 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     }
 }
 
+// Per-task timeline for the measurement build (compiled with TCC_SPMM_TIMELINE by
+// model/timeline.py; the library build leaves this empty and the kernels unchanged). Lane 0 of each
+// workgroup stores, for its task: the workgroup's start, the time its task was found, its end
+// (s_memrealtime, a 100 MHz counter) and its XCC id << 32 | workgroup id, with vector stores.
+struct TaskClock {
+#ifdef TCC_SPMM_TIMELINE
+    unsigned long long start = __builtin_amdgcn_s_memrealtime(), found = 0;
+    __device__ void mapped() { found = __builtin_amdgcn_s_memrealtime(); }
+    __device__ void done(const KernelArgs& a, unsigned task) const {
+        const unsigned long long end = __builtin_amdgcn_s_memrealtime();
+        if (threadIdx.x == 0 && a.stamps) {
+            const unsigned long long xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20); // HW_REG_XCC_ID
+            unsigned long long* out = a.stamps + 4 * std::size_t(task);
+            out[0] = start;
+            out[1] = found;
+            out[2] = end;
+            out[3] = xcc << 32 | blockIdx.x;
+        }
+    }
+#else
+    __device__ void mapped() {}
+    __device__ void done(const KernelArgs&, unsigned) const {}
+#endif
+};
+
 // F128: four waves per SIMD; the 64 accumulators live in ordinary VGPRs and the kernel fits 128
 // registers.
 template <unsigned Addr, unsigned Waves = 1>
 __global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 spmmInt8Kernel128(KernelArgs a) {
+    TaskClock clock;
     unsigned task;
-    if (xcdTask(a, blockIdx.x, task)) runTask<128, Addr, Waves>(a, task);
+    if (xcdTask(a, blockIdx.x, task)) {
+        clock.mapped();
+        runTask<128, Addr, Waves>(a, task);
+        clock.done(a, task);
+    }
 }
 
 // F256: both 128-feature slices of a task in one wave (128 accumulator registers, two waves per
@@ -912,8 +945,13 @@ spmmInt8Kernel128(KernelArgs a) {
 template <unsigned Addr, unsigned Waves = 1>
 __global__ __launch_bounds__(kWave * Waves) __attribute__((amdgpu_waves_per_eu(2, 8))) void
 spmmInt8Kernel256(KernelArgs a) {
+    TaskClock clock;
     unsigned task;
-    if (xcdTask(a, blockIdx.x, task)) runTask<256, Addr, Waves>(a, task);
+    if (xcdTask(a, blockIdx.x, task)) {
+        clock.mapped();
+        runTask<256, Addr, Waves>(a, task);
+        clock.done(a, task);
+    }
 }
 
 // Waves per task: 2 when the plan has few tasks for the chip's wave slots, so that the longest
@@ -997,14 +1035,40 @@ void checkLaunchArguments(const Sw32DeviceView& matrix, const std::int8_t* packe
 
 } // namespace
 
+#ifdef TCC_SPMM_TIMELINE
+// Measurement build only: the stamp buffer of the last launch, grown as needed, and its read-back.
+namespace {
+unsigned long long* gStamps = nullptr;
+std::uint32_t gStampTasks = 0, gStampCapacity = 0;
+
+unsigned long long* timelineStamps(std::uint32_t tasks) {
+    if (tasks > gStampCapacity) {
+        if (gStamps) checkHip(hipFree(gStamps));
+        checkHip(hipMalloc(&gStamps, std::size_t(tasks) * 32));
+        gStampCapacity = tasks;
+    }
+    gStampTasks = tasks;
+    return gStamps;
+}
+} // namespace
+
+extern "C" int tcc_timeline_stamps(unsigned long long* host, std::uint32_t tasks) {
+    if (!gStamps || tasks != gStampTasks || hipDeviceSynchronize() != hipSuccess) return 1;
+    return hipMemcpy(host, gStamps, std::size_t(tasks) * 32, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 2;
+}
+#endif
+
 void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
                     float* output, std::uint32_t rows, std::uint32_t cols, std::uint32_t features,
                     SpmmWorkspace workspace, hipStream_t stream) {
     if (features != 128 && features != 256)
         throw std::invalid_argument("feature dimension must be 128 or 256");
     checkLaunchArguments(matrix, packedX, scales, output);
-    const KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
-                          rows,   cols};
+    KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
+                    rows,   cols};
+#ifdef TCC_SPMM_TIMELINE
+    args.stamps = timelineStamps(matrix.taskCount);
+#endif
     if (features == 128)
         launch<128>(args, stream);
     else
