@@ -8,6 +8,7 @@ import tcc_spmm_amd as T
 
 LINE = 128
 TAIL_WINDOW = 512
+CLASS_THRESHOLDS = (96, 192, 288)  # the kernel's size classes (sizeClass in spmm.hip)
 
 
 def _format(cfg="t300_24_5"):
@@ -46,7 +47,7 @@ def _sequence(fmt, features, xcd, xcds, waves):
     b = _ranges([t[1] for t in tasks], tasks[-1][2], xcds)
     lo, hi = b[xcd], b[xcd + 1]
     w0 = hi - min(hi - lo, TAIL_WINDOW)
-    size_class = lambda t: sum(t[2] - t[1] >= v for v in (96, 192, 288))
+    size_class = lambda t: sum(t[2] - t[1] >= v for v in CLASS_THRESHOLDS)
     order = list(range(lo, w0)) + sorted(range(w0, hi), key=lambda i: -size_class(tasks[i]))
     queue = [tasks[i] for i in order if tasks[i][2] > tasks[i][1]]
     slots = [None] * waves
