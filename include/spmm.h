@@ -27,10 +27,12 @@ struct SpmmWorkspace {
 // output is FP32 row-major. The RW-bucketed SW32 format with its task plan must be uploaded in
 // full. Every output element is overwritten. packedX needs u16 alignment, as in the reference
 // (include/format/int8_features.cuh:11-13); a 16-byte-aligned one (any hipMalloc'd buffer) takes
-// the fastest load path. Throws std::invalid_argument, before any launch, for other feature
-// counts, an odd packedX, a null packedX, scales or output, or a view with null tasks or
-// bucketOffsets (the reference launches and faults instead); std::runtime_error on launch failure.
-// Execution stays asynchronous.
+// the fastest load path. output and workspace.partials need 16-byte alignment (any hipMalloc'd
+// buffer, and any whole-row offset into one, has it): they are written 16 bytes per lane, where the
+// reference stores single floats. Throws std::invalid_argument, before any launch, for other
+// feature counts, an odd packedX, an output or partials base that is not 16-byte aligned, a null
+// packedX, scales or output, or a view with null tasks or bucketOffsets (the reference launches
+// and faults instead); std::runtime_error on launch failure. Execution stays asynchronous.
 // (reference include/spmm.cuh:15-23)
 void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const float* scales,
                     float* output, std::uint32_t rows, std::uint32_t cols, std::uint32_t features,

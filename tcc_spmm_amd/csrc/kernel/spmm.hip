@@ -1031,6 +1031,11 @@ void checkLaunchArguments(const Sw32DeviceView& matrix, const std::int8_t* packe
     // 11-13 states u16 alignment); an odd address cannot be.
     if (reinterpret_cast<std::uintptr_t>(packedX) % 2)
         throw std::invalid_argument("launchSpmmInt8: packedX must be u16-aligned");
+    // Y is written 16 bytes per lane (the reference stores single floats). Any hipMalloc'd buffer,
+    // and any whole-row offset into one, is 16-byte aligned; a base that is not is refused here
+    // rather than left to the GPU's alignment mode.
+    if (reinterpret_cast<std::uintptr_t>(output) % 16)
+        throw std::invalid_argument("launchSpmmInt8: output must be 16-byte aligned");
 }
 
 } // namespace
@@ -1064,6 +1069,9 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
     if (features != 128 && features != 256)
         throw std::invalid_argument("feature dimension must be 128 or 256");
     checkLaunchArguments(matrix, packedX, scales, output);
+    // Partial tiles are written and merged 16 bytes per lane, like Y.
+    if (reinterpret_cast<std::uintptr_t>(workspace.partials) % 16)
+        throw std::invalid_argument("launchSpmmInt8: workspace.partials must be 16-byte aligned");
     KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
                     rows,   cols};
 #ifdef TCC_SPMM_TIMELINE

@@ -141,6 +141,22 @@ def test_device_entry_points_reject_null_buffers_before_any_launch():
     assert st == 3
 
 
+def test_misaligned_output_and_partials_are_rejected_before_any_launch():
+    """Y and the partial tiles are written 16 bytes per lane: a base that is not 16-byte aligned
+    is refused with TCC_INVALID_ARGUMENT before any launch (placeholders, so this runs without a
+    GPU); a u16-aligned packedX is accepted by the same checks."""
+    from tcc_spmm_amd._lib import lib
+    L, P = lib(), PLACEHOLDER
+    view = _placeholder_view()
+    for off in (4, 8, 12):
+        st = L.tcc_launch_spmm_int8(ctypes.byref(view), P, P, P + off, 32, 32, 128, None, None, None)
+        assert st == 1 and b"output must be 16-byte aligned" in L.tcc_last_error()
+        st = L.tcc_launch_spmm_int8_noalloc(ctypes.byref(view), P, P, P + off, 32, 32, 128, 0, None)
+        assert st == 1 and b"output must be 16-byte aligned" in L.tcc_last_error()
+        st = L.tcc_launch_spmm_int8(ctypes.byref(view), P + 2, P, P, 32, 32, 256, P + off, P, None)
+        assert st == 1 and b"partials must be 16-byte aligned" in L.tcc_last_error()
+
+
 def test_noalloc_entry_point_rejects_before_any_launch():
     """launchSpmmInt8NoAlloc checks the feature count and the size of the plan's workspace against
     its fixed scratch before touching the GPU, so both rejections run on a CPU-only host."""
