@@ -124,6 +124,17 @@ def _report(cfg: str) -> None:
             if m.any():
                 print(f"   tasks {name:>11}: {int(m.sum()):6d}, {dur[m].sum() / panels[m].sum() * 1e3:7.1f} ns "
                       f"per panel", flush=True)
+        # Panel throughput over the launch, each task's panels spread evenly over its duration.
+        edges = np.arange(0.0, t1.max() + 100.0, 100.0)
+        rate_bins = np.zeros(len(edges) - 1)
+        for lo, hi, p in zip(t0, t1, panels):
+            if p == 0 or hi <= lo:
+                continue
+            a, b = np.searchsorted(edges, lo, "right") - 1, np.searchsorted(edges, hi, "right") - 1
+            for k in range(a, min(b, len(rate_bins) - 1) + 1):
+                rate_bins[k] += p * (min(hi, edges[k + 1]) - max(lo, edges[k])) / (hi - lo)
+        print("   panels per us, per 100 us of the launch: " +
+              " ".join(f"{v / 100.0:.0f}" for v in rate_bins), flush=True)
         big = (panels >= 288) & (chunks == 1)
         rate = np.median(dur[big] / panels[big]) if big.any() else np.median(dur / np.maximum(panels, 1))
         excess = dur - rate * panels
