@@ -17,6 +17,7 @@ Per configuration and width it reports, after 40 warm-up launches, from one laun
   busy time), its tail (its end minus its last task start) and its end;
 - the time a workgroup takes to find its task (range search and tail window), inside and outside
   the tail window;
+- the panel throughput per 100 us of the launch (each task's panels spread evenly over its duration);
 - the time per panel by task size, and the tasks furthest above (panels x the median time per
   panel of unsplit tasks of 288 panels or more), with their SW's chunk count: a split SW's merging
   task shows up there.
