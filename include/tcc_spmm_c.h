@@ -103,6 +103,10 @@ int tcc_launch_spmm_int8(const tcc_device_view* matrix, const int8_t* packedX, c
 int tcc_launch_spmm_int8_noalloc(const tcc_device_view* matrix, const int8_t* packedX,
                                  const float* scales, float* output, uint32_t rows, uint32_t cols,
                                  uint32_t features, uint32_t partialCount, void* stream);
+/* setSpmmLaunchOverrides (include/spmm.h) — no counterpart in the reference: forces the task form
+ * (taskWaves 0 automatic, 1 or 2) and the 64-bit-addressing instance (forceWide) of later launches,
+ * for tests and measurements. Process-wide. */
+int tcc_set_spmm_launch_overrides(uint32_t taskWaves, int forceWide);
 /* quantizeFeaturesInt8 — reference include/format/int8_features.cuh:9-10. */
 int tcc_quantize_features_int8(const float* x, int8_t* q, float* scale, uint32_t sources,
                                uint32_t features, void* stream);

@@ -93,9 +93,10 @@ def build() -> None:
 
 
 class OracleError(Exception):
-    def __init__(self, code):
-        super().__init__(f"oracle status {code}")
+    def __init__(self, code, message=""):
+        super().__init__(f"oracle status {code}" + (f": {message}" if message else ""))
         self.code = code
+        self.message = message
 
 
 class Oracle:
@@ -350,14 +351,14 @@ class RefFormat:
         st = self.so.ref_canonical_csr(rows, cols, int(off[-1]), off.ctypes.data, src.ctypes.data,
                                        val.ctypes.data, C.byref(h))
         if st:
-            raise OracleError(st)
+            raise OracleError(st, self.so.ref_last_error().decode())
         return self._csr_out(h)[2:]
 
     def load_matrix_market(self, path):
         h = C.c_void_p()
         st = self.so.ref_load_matrix_market(str(path).encode(), C.byref(h))
         if st:
-            raise OracleError(st)
+            raise OracleError(st, self.so.ref_last_error().decode())
         return self._csr_out(h)
 
     def convert(self, rows, cols, offsets, sources, values, bucket=True, digests=False) -> dict:
@@ -370,7 +371,7 @@ class RefFormat:
         st = self.so.ref_convert(rows, cols, int(src.size), off.ctypes.data, src.ctypes.data,
                                  val.ctypes.data, int(bucket), C.byref(h))
         if st:
-            raise OracleError(st)
+            raise OracleError(st, self.so.ref_last_error().decode())
         out = {}
         get = _view if digests else _copy
         for idx, name, dt in self.ARRAYS:

@@ -74,6 +74,7 @@ SIGNATURES = {
     "tcc_launch_spmm_int8_noalloc": (C.c_int, [C.POINTER(DeviceView), C.c_void_p, C.c_void_p,
                                                C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
                                                C.c_uint32, C.c_void_p]),
+    "tcc_set_spmm_launch_overrides": (C.c_int, [C.c_uint32, C.c_int]),
     "tcc_quantize_features_int8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32,
                                              C.c_uint32, C.c_void_p]),
     "tcc_pack_features_int8x16": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,

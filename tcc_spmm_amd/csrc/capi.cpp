@@ -225,6 +225,10 @@ int tcc_launch_spmm_int8_noalloc(const tcc_device_view* matrix, const int8_t* pa
     });
 }
 
+int tcc_set_spmm_launch_overrides(uint32_t taskWaves, int forceWide) {
+    return guarded([&] { setSpmmLaunchOverrides(taskWaves, forceWide != 0); });
+}
+
 int tcc_quantize_features_int8(const float* x, int8_t* q, float* scale, uint32_t sources,
                                uint32_t features, void* stream) {
     return guarded([&] {

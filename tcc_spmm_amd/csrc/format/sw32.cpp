@@ -49,6 +49,33 @@ struct Item {
     std::uint32_t source, mask, first; // first = index of its first Entry in the sorted list
 };
 
+// Entry-level defects of one SW, reported as the reference's converter meets them. It visits the
+// SW's entries in ascending (source, row) order, one cursor per row (src/format/sw32.cpp:96-120):
+// a source at or past `cols` fails when it is first reached, before its entry's value is checked;
+// an entry's value is checked when it is visited; and the entry that follows it in its row must
+// have a larger source, checked right after the value. So within a row, the checks run in entry
+// order and stop at the first defect; across rows, the defect reported is the one with the
+// smallest key (source, row, check), check = 0 column range, 1 value, 2 order of the next entry.
+class SwDefect {
+public:
+    void note(std::uint32_t source, std::uint32_t row, unsigned check) {
+        const std::uint64_t key = (std::uint64_t(source) << 32) | (std::uint64_t(row) << 2) | check;
+        if (key < key_) key_ = key;
+    }
+    void raise() const {
+        if (key_ == kNone) return;
+        switch (unsigned(key_ & 3u)) {
+        case 0: throw std::invalid_argument("source-mask source outside column range");
+        case 1: throw std::invalid_argument("source-mask requires finite nonzero values");
+        default: throw std::invalid_argument("source-mask requires increasing row sources");
+        }
+    }
+
+private:
+    static constexpr std::uint64_t kNone = ~std::uint64_t(0);
+    std::uint64_t key_ = kNone;
+};
+
 void buildBlock(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr, bool bucketed,
                 std::uint32_t swBegin, std::uint32_t swEnd, WindowBlock& out) {
     std::vector<Entry> entries;
@@ -57,21 +84,25 @@ void buildBlock(std::uint32_t rows, std::uint32_t cols, const CsrMatrix& csr, bo
         const std::uint64_t base = std::uint64_t(sw) * 32;
         const std::uint32_t count = std::uint32_t(std::min<std::uint64_t>(32, rows - base));
         entries.clear();
+        SwDefect defect;
         for (std::uint32_t r = 0; r < count; ++r) {
             const std::size_t row = base + r;
             const std::uint32_t e0 = csr.rowOffsets[row], e1 = csr.rowOffsets[row + 1];
             for (std::uint32_t e = e0; e < e1; ++e) {
                 const std::uint32_t s = csr.sourceIds[e];
                 const float v = csr.values[e];
-                if (s >= cols)
-                    throw std::invalid_argument("source-mask source outside column range");
-                if (!std::isfinite(v) || v == 0)
-                    throw std::invalid_argument("source-mask requires finite nonzero values");
-                if (e > e0 && s <= csr.sourceIds[e - 1])
-                    throw std::invalid_argument("source-mask requires increasing row sources");
+                const unsigned check = s >= cols                         ? 0u
+                                       : (!std::isfinite(v) || v == 0)   ? 1u
+                                       : (e + 1 < e1 && csr.sourceIds[e + 1] <= s) ? 2u
+                                                                         : 3u;
+                if (check < 3) {
+                    defect.note(s, r, check);
+                    break; // the rest of this row is never reached
+                }
                 entries.push_back({(std::uint64_t(s) << 5) | r, e});
             }
         }
+        defect.raise();
         std::sort(entries.begin(), entries.end(),
                   [](const Entry& a, const Entry& b) { return a.key < b.key; });
         for (auto& b : buckets) b.clear();

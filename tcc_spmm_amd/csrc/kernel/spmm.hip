@@ -50,6 +50,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
@@ -93,6 +94,7 @@ struct KernelArgs {
     float* partials;
     unsigned* counters;
     unsigned rows, cols;
+    unsigned vec4; // y and partials are 16-byte aligned: stores and merge loads of 16 bytes
 #ifdef TCC_SPMM_TIMELINE
     unsigned long long* stamps; // measurement build only: [taskCount][4], see TaskClock
 #endif
@@ -347,9 +349,16 @@ __device__ __forceinline__ float shiftedMantissa(float s, unsigned keep) {
     return __uint_as_float(r);
 }
 
+// The lane's row and half of the MFMA operands, m = lane & 31 and h = lane >> 5, computed once per
+// task (opaquely, so that the register allocator keeps them rather than recomputing them per panel).
+struct LaneMh {
+    unsigned m, h;
+};
+
 template <bool Wide, unsigned G, unsigned S>
 __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups, unsigned lane,
-                                                const Lds& lds, f32x16 (&acc)[4 * S], unsigned keep) {
+                                                const Lds& lds, f32x16 (&acc)[4 * S], unsigned keep,
+                                                LaneMh mh) {
     const int e = __builtin_amdgcn_frexp_expf(s.scale);
     const bool scaleNormal = e > -126;
     bool exact = true;
@@ -371,12 +380,12 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
         lds.table16[64 * (G < 4 ? G : j) + lane] = static_cast<_Float16>(useF16 ? ap[j] : 0.0f);
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
-    const unsigned m = lane & 31, h = lane >> 5;
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
     // stored as m * 2^-kXShift. For a subnormal scale the bits are not that, but such a panel's
     // table is all zero (scaleNormal above) and the FP32 pass computes it.
     lds.mant[lane & 7] = shiftedMantissa(s.scale, keep);
     waveSync();
+    const unsigned m = mh.m, h = mh.h;
     const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
     const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
 #pragma unroll
@@ -466,6 +475,7 @@ struct TaskWalk {
     Lds lds;
     unsigned redoCount;      // entries in lds.redo
     unsigned keep;           // 0x807FFFFF in a VGPR, for shiftedMantissa
+    LaneMh mh;
 };
 
 // Queues panel `panel` for the FP32 pass when `redo` (wave-uniform) is set. The branch is taken only
@@ -520,12 +530,12 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             // is in order, so computing first would wait for loads issued only half an
             // iteration ago.
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
             ga = groupsAt(min(lo + 2 * k + 2, last));
             loadStage<G, S, Ld, false>(ld, mSecond, ga, lane, sa);
             __builtin_amdgcn_sched_barrier(0);
             sb.scale = __uint_as_float(pairHalf<0>(__float_as_uint(sc)));
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
             sa.scale = __uint_as_float(pairHalf<1>(__float_as_uint(sc)));
             pair = next;
             mFirst = pairPanel<0>(pair);
@@ -549,7 +559,7 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             g2 = groupsAt(p);
             m2 = ld.meta8(p, lane);
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
             ga = g1;
             loadStage<G, S>(ld, m1, ga, lane, sa);
             p = min(p + 1, last);
@@ -558,10 +568,10 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             g2 = groupsAt(p);
             m2 = ld.meta8(p, lane);
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
         }
     }
-    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep));
+    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
 }
 
 template <unsigned S, class Ld>
@@ -573,7 +583,9 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
     // rematerialised literal per use.
     unsigned keep;
     asm("v_mov_b32 %0, 0x807fffff" : "=v"(keep));
-    TaskWalk w{offsets, begin, end, lane, lds, 0u, keep};
+    LaneMh mh;
+    asm("v_and_b32 %0, 31, %2\n\tv_lshrrev_b32 %1, 5, %2" : "=v"(mh.m), "=v"(mh.h) : "v"(lane));
+    TaskWalk w{offsets, begin, end, lane, lds, 0u, keep, mh};
     auto clipLo = [&](unsigned t) { return max(offsets[t], begin); };
     auto clipHi = [&](unsigned t) { return min(offsets[t], end); };
     walkPanels<0, S>(ld, w, clipLo(1), clipHi(2), acc);
@@ -592,9 +604,37 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
     }
 }
 
+// Four consecutive floats of Y or of the partial tiles. Vec4: one 16-byte access (the buffer's
+// base is 16-byte aligned, which every row offset keeps); otherwise four dword accesses, for a base
+// that is only float-aligned (the reference stores single floats, src/kernel/spmm_kernel.cuh:
+// 236-245, so it accepts one).
+template <bool Vec4>
+__device__ __forceinline__ void store4(float* p, const f32x4& v, bool nontemporal) {
+    if constexpr (Vec4) {
+        if (nontemporal)
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+        else
+            *reinterpret_cast<f32x4*>(p) = v;
+    } else {
+#pragma unroll
+        for (unsigned t = 0; t < 4; ++t) {
+            if (nontemporal)
+                __builtin_nontemporal_store(v[t], p + t);
+            else
+                p[t] = v[t];
+        }
+    }
+}
+template <bool Vec4>
+__device__ __forceinline__ f32x4 load4(const float* p) {
+    if constexpr (Vec4) return *reinterpret_cast<const f32x4*>(p);
+    else return f32x4{p[0], p[1], p[2], p[3]};
+}
+
 // Store row `row` (lane & 31) of the accumulators: per tile i the lane holds the 16 features
 // 16 (2i + h) .. + 15 of the slice, block b / register 4i + j holding feature 2j + (b >> 1) +
 // 8 (b & 1) of that tile.
+template <bool Vec4>
 __device__ __forceinline__ void storeRow(const f32x16 (&acc)[4], float* rowBase, unsigned h,
                                          bool nontemporal) {
 #pragma unroll
@@ -610,10 +650,7 @@ __device__ __forceinline__ void storeRow(const f32x16 (&acc)[4], float* rowBase,
                 const unsigned rem = o - 8 * hiHalf;
                 v[t] = acc[(rem & 1u) * 2 + hiHalf][4 * i + (rem >> 1)];
             }
-            if (nontemporal)
-                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + 4 * q));
-            else
-                *reinterpret_cast<f32x4*>(dst + 4 * q) = v;
+            store4<Vec4>(dst + 4 * q, v, nontemporal);
         }
     }
 }
@@ -691,15 +728,17 @@ __device__ __forceinline__ unsigned tailTask(const Sw32Task* tasks, unsigned w0,
 }
 
 // Boundaries x and x + 1 of the panel-balanced ranges: the first task starting at or past k/8 of
-// the panels (k = x, x + 1; `count` when none does). Lanes 32h .. 32h + 31 search boundary x + h
+// the panels, measured from the first task's begin (k = x, x + 1; `count` when none does; a view
+// over a later part of a plan's task list starts past panel 0). Lanes 32h .. 32h + 31 search boundary x + h
 // together: each step probes 32 evenly spaced tasks of the half's interval [l, r] (task r is known
 // to qualify; r = count stands for past the end) and keeps the stretch between the last probe
 // below the target and the first one at or past it, so a search takes about log32(T) dependent
 // loads instead of log2(T). Returns the boundary of each lane's half.
 __device__ __forceinline__ unsigned panelBound(const Sw32Task* tasks, unsigned count,
-                                               std::uint64_t panels, unsigned x, unsigned lane) {
+                                               unsigned first, std::uint64_t panels, unsigned x,
+                                               unsigned lane) {
     const unsigned h = lane >> 5, j = lane & 31;
-    const unsigned target = unsigned(panels * (x + h) / 8);
+    const unsigned target = first + unsigned(panels * (x + h) / 8);
     unsigned l = 0, r = count;
     while (__builtin_amdgcn_ballot_w64(l < r) != 0) {
         const unsigned stride = (r - l + 31) / 32; // 32 probes cover [l, r): r - l <= 32 stride
@@ -726,11 +765,11 @@ __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsig
     for (unsigned k = 0; k <= 8; ++k) first[k] = beginOf(equalBound(count, k));
 #pragma unroll
     for (unsigned k = 0; k < 8; ++k) maxPanels = max(maxPanels, first[k + 1] - first[k]);
-    const std::uint64_t panels = first[8];
+    const std::uint64_t panels = first[8] - first[0];
     unsigned lo = equalBound(count, x), hi = equalBound(count, x + 1);
     if (std::uint64_t(maxPanels) * 8 * 100 > panels * 103) {
         const unsigned reach = spareWorkgroups(count) / 2;
-        const unsigned searched = panelBound(tasks, count, panels, x, lane);
+        const unsigned searched = panelBound(tasks, count, first[0], panels, x, lane);
         const unsigned k = x + (lane >> 5), eq = equalBound(count, k);
         const unsigned b = (k == 0 || k == 8) ? eq : min(max(searched, eq > reach ? eq - reach : 0u), eq + reach);
         lo = __builtin_amdgcn_readlane(b, 0);
@@ -741,6 +780,64 @@ __device__ __forceinline__ bool xcdTask(const KernelArgs& a, unsigned bid, unsig
     const unsigned n = min(hi - lo, kTailWindow), w0 = hi - n;
     if (task >= w0) task = tailTask(tasks, w0, n, task - w0, lane);
     return true;
+}
+
+// Merge of slice k of a split SW by the task that took its last ticket (reference
+// src/kernel/spmm_kernel.cuh:250-282): Y = the SW's partial tiles summed in partialIds order,
+// starting from 0.0f, one row group (8 rows x 128 columns) at a time. Lane L sums the four 16-byte
+// column blocks (L & 7) + 8j, j < 4, of row L >> 3. The group's tile ids are loaded once (one per
+// lane, broadcast by readlane), and the loads of kMergeBatch tiles are issued before they are added
+// in order, so a merge of many chunks waits for one load latency per batch, not per tile. Per element
+// the additions run in partialIds order whatever the batch, so Y is bitwise the same for any batch.
+template <unsigned Features, bool Vec4>
+__device__ __forceinline__ void mergeSlice(const KernelArgs& a, const Sw32Task& task, unsigned k,
+                                           unsigned lane) {
+    constexpr unsigned kMergeBatch = 4;
+    const unsigned sw = task.sw;
+    const unsigned mrow = lane >> 3, mcol = k * kSlice + (lane & 7) * 4;
+#pragma unroll 1
+    for (unsigned g = 0; g < 4; ++g) {
+        const Sw32ReduceRange red = a.m.reductions[task.reduceFirst + g];
+        const unsigned row0 = sw * 32 + g * 8;
+        if (row0 >= a.rows) continue;
+        f32x4 sum[4];
+#pragma unroll
+        for (unsigned j = 0; j < 4; ++j) sum[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        auto tileRow = [&](unsigned id) {
+            return a.partials + (std::size_t(id) * 8 + mrow) * Features + mcol;
+        };
+#pragma unroll 1
+        for (unsigned base = red.begin; base < red.end; base += kWave) {
+            const unsigned items = min(red.end - base, kWave);
+            const unsigned ids = a.m.partialIds[base + min(lane, items - 1)];
+            unsigned i = 0;
+#pragma unroll 1
+            for (; i + kMergeBatch <= items; i += kMergeBatch) {
+                f32x4 v[kMergeBatch][4];
+#pragma unroll
+                for (unsigned u = 0; u < kMergeBatch; ++u) {
+                    const float* src = tileRow(__builtin_amdgcn_readlane(ids, i + u));
+#pragma unroll
+                    for (unsigned j = 0; j < 4; ++j) v[u][j] = load4<Vec4>(src + 32 * j);
+                }
+#pragma unroll
+                for (unsigned u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+                    for (unsigned j = 0; j < 4; ++j) sum[j] += v[u][j];
+            }
+#pragma unroll 1
+            for (; i < items; ++i) {
+                const float* src = tileRow(__builtin_amdgcn_readlane(ids, i));
+#pragma unroll
+                for (unsigned j = 0; j < 4; ++j) sum[j] += load4<Vec4>(src + 32 * j);
+            }
+        }
+        if (row0 + mrow < a.rows) {
+            float* yr = a.y + std::size_t(row0 + mrow) * Features + mcol;
+#pragma unroll
+            for (unsigned j = 0; j < 4; ++j) store4<Vec4>(yr + 32 * j, sum[j], false);
+        }
+    }
 }
 
 // One task over all S = Features / 128 slices of its SW, by `Waves` waves of one workgroup. With
@@ -805,26 +902,35 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     }
 
     const unsigned row = lane & 31, h = lane >> 5;
+    // Write-back. An unsplit task stores its rows of Y (nontemporal: nothing reads them again in this
+    // launch); a split task stores the row groups of task.mask as 8-row partial tiles. One store site
+    // for both, so that the accumulators are dead once it is passed.
+    const bool split = task.partial != kNoPartial;
+    const unsigned rw = row >> 3;
+    float* dst;
+    bool mine;
+    if (!split) {
+        const unsigned r = sw * 32 + row;
+        mine = r < a.rows;
+        dst = a.y + std::size_t(r) * Features;
+    } else {
+        mine = (task.mask >> rw) & 1u;
+        const std::size_t tile = task.partial + __popc(task.mask & ((1u << rw) - 1u));
+        dst = a.partials + (tile * 8 + (row & 7)) * Features;
+    }
     auto sub = [&](unsigned k) -> const f32x16(&)[4] {
         return *reinterpret_cast<const f32x16(*)[4]>(&acc[4 * k]);
     };
-    if (task.partial == kNoPartial) {
-        const unsigned r = sw * 32 + row;
-        if (r < a.rows) {
+    if (mine) {
+        if (a.vec4) {
 #pragma unroll
-            for (unsigned k = 0; k < S; ++k)
-                storeRow(sub(k), a.y + std::size_t(r) * Features + k * kSlice, h, true);
+            for (unsigned k = 0; k < S; ++k) storeRow<true>(sub(k), dst + k * kSlice, h, !split);
+        } else {
+#pragma unroll
+            for (unsigned k = 0; k < S; ++k) storeRow<false>(sub(k), dst + k * kSlice, h, !split);
         }
-        return;
     }
-    const unsigned rw = row >> 3;
-    if ((task.mask >> rw) & 1u) {
-        const std::size_t tile = task.partial + __popc(task.mask & ((1u << rw) - 1u));
-#pragma unroll
-        for (unsigned k = 0; k < S; ++k)
-            storeRow(sub(k), a.partials + (tile * 8 + (row & 7)) * Features + k * kSlice, h,
-                     false);
-    }
+    if (!split) return;
 
     // Completion tickets, one per slice: the acq_rel RMW at agent scope publishes this task's
     // partial tiles and, for the last arriver, makes every other task's tiles visible (the XCD L2s
@@ -844,58 +950,10 @@ __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex)
     for (unsigned k = 0; k < S; ++k) {
         if (!lastFlag[k]) continue;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // Merge the slice, one row group (8 rows x 128 columns) at a time: lane L sums the four
-        // 16-byte column blocks (L & 7) + 8j, j < 4, of row L >> 3, adding the partial tiles in
-        // partialIds (task) order starting from 0.0f. The group's tile ids are loaded once (one per
-        // lane, broadcast by readlane), and the loads of kMergeBatch tiles are issued before they
-        // are added, so a merge of many chunks waits for one load latency per batch, not per tile.
-        // More than two tiles in flight spill at F128.
-        constexpr unsigned kMergeBatch = 2;
-        const unsigned mrow = lane >> 3, mcol = k * kSlice + (lane & 7) * 4;
-#pragma unroll 1
-        for (unsigned g = 0; g < 4; ++g) {
-            const Sw32ReduceRange red = a.m.reductions[task.reduceFirst + g];
-            const unsigned row0 = sw * 32 + g * 8;
-            if (row0 >= a.rows) continue;
-            f32x4 sum[4];
-#pragma unroll
-            for (unsigned j = 0; j < 4; ++j) sum[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            auto tileRow = [&](unsigned id) {
-                return reinterpret_cast<const f32x4*>(a.partials + (std::size_t(id) * 8 + mrow) * Features +
-                                                      mcol);
-            };
-#pragma unroll 1
-            for (unsigned base = red.begin; base < red.end; base += kWave) {
-                const unsigned items = min(red.end - base, kWave);
-                const unsigned ids = a.m.partialIds[base + min(lane, items - 1)];
-                unsigned i = 0;
-#pragma unroll 1
-                for (; i + kMergeBatch <= items; i += kMergeBatch) {
-                    f32x4 v[kMergeBatch][4];
-#pragma unroll
-                    for (unsigned u = 0; u < kMergeBatch; ++u) {
-                        const f32x4* src = tileRow(__builtin_amdgcn_readlane(ids, i + u));
-#pragma unroll
-                        for (unsigned j = 0; j < 4; ++j) v[u][j] = src[8 * j];
-                    }
-#pragma unroll
-                    for (unsigned u = 0; u < kMergeBatch; ++u)
-#pragma unroll
-                        for (unsigned j = 0; j < 4; ++j) sum[j] += v[u][j];
-                }
-#pragma unroll 1
-                for (; i < items; ++i) {
-                    const f32x4* src = tileRow(__builtin_amdgcn_readlane(ids, i));
-#pragma unroll
-                    for (unsigned j = 0; j < 4; ++j) sum[j] += src[8 * j];
-                }
-            }
-            if (row0 + mrow < a.rows) {
-                f32x4* yr = reinterpret_cast<f32x4*>(a.y + std::size_t(row0 + mrow) * Features + mcol);
-#pragma unroll
-                for (unsigned j = 0; j < 4; ++j) yr[8 * j] = sum[j];
-            }
-        }
+        if (a.vec4)
+            mergeSlice<Features, true>(a, task, k, lane);
+        else
+            mergeSlice<Features, false>(a, task, k, lane);
     }
 }
 
@@ -954,19 +1012,43 @@ spmmInt8Kernel256(KernelArgs a) {
     }
 }
 
+constexpr int kMaxDevices = 64;
+
+// Launch choices forced by setSpmmLaunchOverrides or, initially, the environment (read once).
+std::once_flag overridesRead;
+std::atomic<unsigned> forcedWaves{0}; // 0: chosen per launch
+std::atomic<bool> forcedWide{false};
+
+void readOverridesOnce() {
+    std::call_once(overridesRead, [] {
+        if (const char* w = std::getenv("TCC_SPMM_TASK_WAVES"))
+            forcedWaves.store(std::strcmp(w, "2") == 0 ? 2u : 1u);
+        if (std::getenv("TCC_SPMM_FORCE_WIDE")) forcedWide.store(true);
+    });
+}
+
+// Compute units of the current device, queried once per device (0 when unknown).
+std::atomic<int> deviceCuCount[kMaxDevices];
+
+int currentDeviceCus() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return 0;
+    int cus = deviceCuCount[device].load(std::memory_order_relaxed);
+    if (cus == 0 &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess)
+        deviceCuCount[device].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
 // Waves per task: 2 when the plan has few tasks for the chip's wave slots, so that the longest
 // tasks, not the bandwidth, set the launch time; else 1. Measured crossovers on MI355X (256 CUs;
 // wave slots = CUs x 4 SIMDs x the kernel's waves per SIMD, 4 at F128 and 2 at F256): F128 gains
 // below about 3 tasks per slot (-39% at 250 tasks, -6% at 8,790, even at 12,500, +3% at 38,281),
-// F256 below about half a task per slot (-26% at 1,000 tasks, +1% at 1,875). TCC_SPMM_TASK_WAVES=1
-// or 2 overrides the choice (tests and measurements).
+// F256 below about half a task per slot (-26% at 1,000 tasks, +1% at 1,875).
 unsigned taskWaves(unsigned taskCount, unsigned features) {
-    if (const char* forced = std::getenv("TCC_SPMM_TASK_WAVES"))
-        return std::strcmp(forced, "2") == 0 ? 2u : 1u;
-    int device = 0, cus = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-        return 1;
+    if (const unsigned forced = forcedWaves.load()) return forced;
+    const int cus = currentDeviceCus();
+    if (cus <= 0) return 1;
     const std::uint64_t slots = std::uint64_t(cus) * 4 * (features == 128 ? 4 : 2);
     const std::uint64_t limit = features == 128 ? 3 * slots : slots / 2;
     return taskCount < limit ? 2u : 1u;
@@ -976,11 +1058,10 @@ template <unsigned Features>
 void launch(const KernelArgs& args, hipStream_t stream) {
     // Buffer addressing needs the packed X and the scales within 32-bit byte offsets, with room for
     // the padding sentinel to land out of range, and 16-byte aligned X tiles. A packed X that is
-    // only u16-aligned takes the 64-bit instance with 2-byte tile loads. TCC_SPMM_FORCE_WIDE
-    // selects the 64-bit instance for any size (used by the tests).
+    // only u16-aligned takes the 64-bit instance with 2-byte tile loads. setSpmmLaunchOverrides
+    // can select the 64-bit instance for any size (used by the tests).
     const bool misaligned = reinterpret_cast<std::uintptr_t>(args.packedX) % 16 != 0;
-    const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull ||
-                      std::getenv("TCC_SPMM_FORCE_WIDE") != nullptr;
+    const bool wide = std::uint64_t(args.cols) * Features > 0xFFFFFF00ull || forcedWide.load();
     const dim3 grid(args.m.taskCount + 8 * spareWorkgroups(args.m.taskCount), 1);
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kWave), 0, stream, args); };
     auto go2 = [&](auto kernel) {
@@ -1031,11 +1112,10 @@ void checkLaunchArguments(const Sw32DeviceView& matrix, const std::int8_t* packe
     // 11-13 states u16 alignment); an odd address cannot be.
     if (reinterpret_cast<std::uintptr_t>(packedX) % 2)
         throw std::invalid_argument("launchSpmmInt8: packedX must be u16-aligned");
-    // Y is written 16 bytes per lane (the reference stores single floats). Any hipMalloc'd buffer,
-    // and any whole-row offset into one, is 16-byte aligned; a base that is not is refused here
-    // rather than left to the GPU's alignment mode.
-    if (reinterpret_cast<std::uintptr_t>(output) % 16)
-        throw std::invalid_argument("launchSpmmInt8: output must be 16-byte aligned");
+    // Y is written as floats (16 bytes per lane when Y and the partials are 16-byte aligned, one
+    // float per store otherwise), so a float-aligned base is accepted, as in the reference.
+    if (reinterpret_cast<std::uintptr_t>(output) % alignof(float))
+        throw std::invalid_argument("launchSpmmInt8: output must be float-aligned");
 }
 
 } // namespace
@@ -1069,11 +1149,16 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
     if (features != 128 && features != 256)
         throw std::invalid_argument("feature dimension must be 128 or 256");
     checkLaunchArguments(matrix, packedX, scales, output);
-    // Partial tiles are written and merged 16 bytes per lane, like Y.
-    if (reinterpret_cast<std::uintptr_t>(workspace.partials) % 16)
-        throw std::invalid_argument("launchSpmmInt8: workspace.partials must be 16-byte aligned");
+    readOverridesOnce();
+    if (reinterpret_cast<std::uintptr_t>(workspace.partials) % alignof(float))
+        throw std::invalid_argument("launchSpmmInt8: workspace.partials must be float-aligned");
+    // Y and the partial tiles move 16 bytes per lane when both bases allow it (any hipMalloc'd
+    // buffer and any whole-row offset into one does), else one float per access; Y is bitwise
+    // the same either way.
+    const bool vec4 = (reinterpret_cast<std::uintptr_t>(output) |
+                       reinterpret_cast<std::uintptr_t>(workspace.partials)) % 16 == 0;
     KernelArgs args{matrix, packedX, scales, output, workspace.partials, workspace.counters,
-                    rows,   cols};
+                    rows,   cols,    unsigned(vec4)};
 #ifdef TCC_SPMM_TIMELINE
     args.stamps = timelineStamps(matrix.taskCount);
 #endif
@@ -1082,6 +1167,14 @@ void launchSpmmInt8(Sw32DeviceView matrix, const std::int8_t* packedX, const flo
     else
         launch<256>(args, stream);
     checkHip(hipGetLastError());
+}
+
+void setSpmmLaunchOverrides(std::uint32_t taskWaves, bool forceWide) {
+    if (taskWaves > 2)
+        throw std::invalid_argument("setSpmmLaunchOverrides: taskWaves must be 0, 1 or 2");
+    readOverridesOnce(); // so that a later first launch keeps these rather than the environment's
+    forcedWaves.store(taskWaves);
+    forcedWide.store(forceWide);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1094,7 +1187,6 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
-constexpr int kMaxDevices = 64;
 std::mutex scratchLock;
 void* scratchAddress[kMaxDevices]; // device address of `scratch` per device, found once
 

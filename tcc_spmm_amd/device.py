@@ -7,6 +7,7 @@ missing the calls raise.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 from dataclasses import dataclass
 
@@ -177,6 +178,19 @@ def launch_spmm_int8_noalloc(view: DeviceView, packed_x: torch.Tensor, scales: t
                                              _stream_ptr(stream)))
 
 
+@contextlib.contextmanager
+def launch_overrides(task_waves: int = 0, force_wide: bool = False):
+    """setSpmmLaunchOverrides (include/spmm.h; no counterpart in the reference) for the body of a
+    with-block, then back to automatic choices: task_waves 0 (automatic), 1 or 2 waves per task;
+    force_wide selects the 64-bit-addressing kernel instance for any size. Process-wide; for tests
+    and measurements."""
+    check(lib().tcc_set_spmm_launch_overrides(task_waves, int(force_wide)))
+    try:
+        yield
+    finally:
+        check(lib().tcc_set_spmm_launch_overrides(0, 0))
+
+
 class TorchDeviceMatrix:
     """Uploads every array of a bucketed Sw32HostFormat into torch tensors and builds the view.
 
@@ -200,7 +214,7 @@ class TorchDeviceMatrix:
             self.tensors[name] = torch.from_numpy(raw).to(device) if raw.size else None
         self.task_count = int(arrs["tasks"].shape[0])
         windows = int(arrs["window_offsets"].shape[0]) - 1
-        k = fmt.partial_count
+        k = self.partial_count = fmt.partial_count
         if k:
             self.partials = torch.empty(k * 8 * features, dtype=torch.float32, device=device)
             self.counters = torch.zeros(windows * (features // 128), dtype=torch.int32,
@@ -226,6 +240,18 @@ class TorchDeviceMatrix:
                          self.workspace(), stream)
         return output
 
+    def spmm_noalloc(self, packed_x: torch.Tensor, scales: torch.Tensor,
+                     output: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """launch_spmm_int8_noalloc with the uploaded plan's own partial count (a wrong count is
+        undefined behaviour in the free function, which cannot check it)."""
+        if output is None:
+            output = torch.empty((self.rows, self.features), dtype=torch.float32,
+                                 device=packed_x.device)
+        _require_same_device(self.device, packed_x)
+        launch_spmm_int8_noalloc(self.view, packed_x, scales, output, self.rows, self.cols,
+                                 self.features, self.partial_count, stream)
+        return output
+
 
 class NativeDeviceMatrix:
     """DeviceMatrix owned by the library (tcc_device_matrix_*): hipMalloc'd arrays + workspace."""
@@ -238,6 +264,7 @@ class NativeDeviceMatrix:
         check(lib().tcc_device_matrix_view(self._h, C.byref(self.view), C.byref(p), C.byref(c)))
         self.partials_ptr, self.counters_ptr = p.value or 0, c.value or 0
         self.rows, self.cols, self.features = fmt.rows, fmt.cols, features
+        self.partial_count = fmt.partial_count
         # The library uploads to the device current at creation.
         self.device = torch.device("cuda", torch.cuda.current_device())
 
@@ -254,4 +281,12 @@ class NativeDeviceMatrix:
                                          _ptr(output), self.rows, self.cols, self.features,
                                          self.partials_ptr, self.counters_ptr,
                                          _stream_ptr(stream)))
+        return output
+
+    def spmm_noalloc(self, packed_x: torch.Tensor, scales: torch.Tensor, output: torch.Tensor,
+                     stream=None) -> torch.Tensor:
+        """launch_spmm_int8_noalloc with the uploaded plan's own partial count."""
+        _require_same_device(self.device, packed_x)
+        launch_spmm_int8_noalloc(self.view, packed_x, scales, output, self.rows, self.cols,
+                                 self.features, self.partial_count, stream)
         return output

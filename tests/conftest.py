@@ -57,3 +57,16 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def launch_overrides():
+    """setSpmmLaunchOverrides for one test (task form, 64-bit instance); automatic choices again
+    afterwards. Calling it needs no GPU."""
+    from tcc_spmm_amd._lib import check, lib
+
+    def set_overrides(task_waves=0, force_wide=False):
+        check(lib().tcc_set_spmm_launch_overrides(int(task_waves), int(bool(force_wide))))
+
+    yield set_overrides
+    set_overrides(0, False)

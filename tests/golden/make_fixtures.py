@@ -10,7 +10,11 @@ convertCsrToSw32 output (all nine arrays, partialCount) for the synthetic config
 and c5 (c4 shares c3's matrix), and of its makeCanonicalCsr output for a non-canonical input of c2's
 size (noncanonical_from below). The matrices come from this repository's deterministic generator.
 
-Run from the repository root:  python tests/golden/make_fixtures.py
+It also writes tests/golden/sw32_defects.json: small CSRs with several entry defects in one SW and
+the exception the reference's convertCsrToSw32 raises for each (class and message).
+
+Run from the repository root:  python tests/golden/make_fixtures.py  (add --defects-only to write
+only sw32_defects.json)
 """
 from __future__ import annotations
 
@@ -151,6 +155,45 @@ def mtx_cases():
     }
 
 
+def defect_cases():
+    """(name, rows, cols, rows_entries) canonical-shaped CSRs with several entry defects in ONE SW,
+    each row a list of (source, value). The reference's converter meets them in ascending
+    (source, row) order, not in row order, so these pin which message it reports."""
+    nan, inf = float("nan"), float("inf")
+    return [
+        ("defect_range_then_zero", 2, 4, [[(5, 1.0)], [(0, 0.0)]]),
+        ("defect_order_then_nan", 2, 4, [[(0, 1.0), (2, 1.0), (1, 1.0)], [(1, nan)]]),
+        ("defect_zero_then_duplicate", 6, 8, [[(3, 0.0)], [], [], [], [], [(1, 1.0), (1, 1.0)]]),
+        ("defect_range_rows_then_inf", 32, 6,
+         [[(0, 1.0), (7, 1.0)]] + [[]] * 2 + [[(2, 1.0), (9, 1.0), (8, 1.0)]] + [[]] * 27 +
+         [[(1, inf)]]),
+        ("defect_late_row_small_source", 21, 16,
+         [[(10, 1.0), (11, 0.0)]] + [[]] * 19 + [[(5, 1.0), (4, 1.0)]]),
+        ("defect_same_source_rows", 3, 8, [[(2, 1.0)], [(3, 1.0), (2, 1.0)], [(3, 0.0)]]),
+        ("defect_range_vs_value", 3, 8, [[(9, 1.0)], [(8, 1.0)], [(7, 0.0)]]),
+    ]
+
+
+def write_defects(ref):
+    """tests/golden/sw32_defects.json: each defect case's input and the reference's exception."""
+    out = []
+    for name, rows, cols, entries in defect_cases():
+        off = np.concatenate([[0], np.cumsum([len(r) for r in entries])]).astype(np.uint32)
+        src = np.array([s for r in entries for s, _ in r], np.uint32)
+        val = np.array([v for r in entries for _, v in r], np.float32)
+        try:
+            ref.convert(rows, cols, off, src, val, True)
+            code, message = 0, ""
+        except OracleError as e:
+            code, message = e.code, e.message
+        out.append({"name": name, "rows": rows, "cols": cols, "offsets": off.tolist(),
+                    "sources": src.tolist(), "values": [repr(float(v)) for v in val],
+                    "status": code, "message": message})
+    path = OUT / "sw32_defects.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"wrote {path}: {len(out)} cases")
+
+
 DIGEST_CONFIGS = ("c1", "c2", "c5", "c3")
 
 
@@ -206,6 +249,9 @@ def main():
     if not RefFormat.available():
         raise SystemExit("oracle/_ref/libref_format.so was not built (is /root/reference present?)")
     ref = RefFormat()
+    write_defects(ref)
+    if "--defects-only" in sys.argv:
+        return
     rng = np.random.default_rng(20261201)
     store = {}
     names = []

@@ -141,20 +141,22 @@ def test_device_entry_points_reject_null_buffers_before_any_launch():
     assert st == 3
 
 
-def test_misaligned_output_and_partials_are_rejected_before_any_launch():
-    """Y and the partial tiles are written 16 bytes per lane: a base that is not 16-byte aligned
-    is refused with TCC_INVALID_ARGUMENT before any launch (placeholders, so this runs without a
-    GPU); a u16-aligned packedX is accepted by the same checks."""
+def test_output_and_partials_must_be_float_aligned():
+    """Y and the partial tiles are written as floats, so any float-aligned base is accepted, as in
+    the reference (src/kernel/spmm_kernel.cuh:236-245; the GPU test
+    test_spmm_float_aligned_output_and_partials runs +4/+8/+12-byte bases). A base that is not
+    float-aligned is refused with TCC_INVALID_ARGUMENT before any launch (placeholders, so this
+    runs without a GPU; only offsets that must be refused are passed here)."""
     from tcc_spmm_amd._lib import lib
     L, P = lib(), PLACEHOLDER
     view = _placeholder_view()
-    for off in (4, 8, 12):
+    for off in (1, 2, 3, 6, 13):
         st = L.tcc_launch_spmm_int8(ctypes.byref(view), P, P, P + off, 32, 32, 128, None, None, None)
-        assert st == 1 and b"output must be 16-byte aligned" in L.tcc_last_error()
+        assert st == 1 and b"output must be float-aligned" in L.tcc_last_error()
         st = L.tcc_launch_spmm_int8_noalloc(ctypes.byref(view), P, P, P + off, 32, 32, 128, 0, None)
-        assert st == 1 and b"output must be 16-byte aligned" in L.tcc_last_error()
-        st = L.tcc_launch_spmm_int8(ctypes.byref(view), P + 2, P, P, 32, 32, 256, P + off, P, None)
-        assert st == 1 and b"partials must be 16-byte aligned" in L.tcc_last_error()
+        assert st == 1 and b"output must be float-aligned" in L.tcc_last_error()
+        st = L.tcc_launch_spmm_int8(ctypes.byref(view), P + 2, P, P + 4, 32, 32, 256, P + off, P, None)
+        assert st == 1 and b"partials must be float-aligned" in L.tcc_last_error()
 
 
 def test_noalloc_entry_point_rejects_before_any_launch():
@@ -222,3 +224,14 @@ def test_null_outputs_and_arrays_are_rejected():
             L.tcc_sw32_free(fmt)
     finally:
         L.tcc_csr_free(h)
+
+
+def test_launch_overrides_hook(launch_overrides):
+    """setSpmmLaunchOverrides takes 0 (automatic), 1 or 2 waves per task and rejects other counts;
+    it touches no GPU."""
+    from tcc_spmm_amd._lib import lib
+    for waves in (0, 1, 2):
+        assert lib().tcc_set_spmm_launch_overrides(waves, 0) == 0
+    assert lib().tcc_set_spmm_launch_overrides(1, 1) == 0
+    assert lib().tcc_set_spmm_launch_overrides(3, 0) == 1
+    assert b"taskWaves" in lib().tcc_last_error()

@@ -194,3 +194,32 @@ def test_conversion_reports_first_defective_sw(ref_format):
         T.convert_csr_to_sw32(rows, cols, raw)
     with pytest.raises(OracleError):
         ref_format.convert(rows, cols, off, src, val)
+
+
+def _defect_cases():
+    import json
+    import pathlib
+    path = pathlib.Path(__file__).resolve().parent / "golden" / "sw32_defects.json"
+    return json.loads(path.read_text())
+
+
+@pytest.mark.parametrize("case", _defect_cases(), ids=lambda c: c["name"])
+def test_conversion_reports_reference_first_defect_within_sw(case, request):
+    """Several entry defects in one SW (tests/golden/sw32_defects.json, written from the reference's
+    compiled converter): the product raises the reference's exception class and message. The
+    reference meets entries in ascending (source, row) order (src/format/sw32.cpp:96-120), so a
+    row-order scan would report a different defect for most of these."""
+    rows, cols = case["rows"], case["cols"]
+    off = np.array(case["offsets"], np.uint32)
+    src = np.array(case["sources"], np.uint32)
+    val = np.array([float(v) for v in case["values"]], np.float32)
+    assert case["status"] == 1 and case["message"]
+    raw = T.csr_from_arrays(rows, cols, off, src, val)
+    with pytest.raises(ValueError) as got:
+        T.convert_csr_to_sw32(rows, cols, raw)
+    assert str(got.value) == case["message"]
+    from oracle import RefFormat
+    if RefFormat.available():  # the live reference agrees with the committed fixture
+        with pytest.raises(OracleError) as ref:
+            RefFormat().convert(rows, cols, off, src, val)
+        assert (ref.value.code, ref.value.message) == (1, case["message"])

@@ -13,10 +13,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("entry", ["workspace", "noalloc"])
 @pytest.mark.parametrize("feats,waves", [(128, "1"), (128, "2"), (256, "1")])
-def test_spmm_replays_from_a_hip_graph(gpu, entry, feats, waves, monkeypatch):
+def test_spmm_replays_from_a_hip_graph(gpu, entry, feats, waves, launch_overrides):
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix, launch_spmm_int8_noalloc
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", waves)
+    launch_overrides(task_waves=int(waves))
     print(f"graph case: {entry} F{feats} waves {waves}", flush=True)
     csr = T.synth_csr("c2")
     fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)

@@ -32,8 +32,8 @@ def _many_chunk_csr():
 
 @pytest.mark.parametrize("waves", ["1", "2"])
 @pytest.mark.parametrize("feats", [128, 256])
-def test_merge_of_many_chunks(oracle, gpu, feats, waves, monkeypatch):
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", waves)
+def test_merge_of_many_chunks(oracle, gpu, feats, waves, launch_overrides):
+    launch_overrides(task_waves=int(waves))
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix
     rows, cols, off, src, val = _many_chunk_csr()

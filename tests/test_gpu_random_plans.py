@@ -56,8 +56,8 @@ def _random_csr(seed):
 
 @pytest.mark.parametrize("waves", ["1", "2"])
 @pytest.mark.parametrize("seed", range(12))
-def test_random_plans_against_the_oracle(oracle, gpu, seed, waves, monkeypatch):
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", waves)
+def test_random_plans_against_the_oracle(oracle, gpu, seed, waves, launch_overrides):
+    launch_overrides(task_waves=int(waves))
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix
     rows, cols, off, src, val = _random_csr(1000 + seed)

@@ -94,12 +94,12 @@ def test_spmm_c2_full(oracle, gpu, feats):
 
 @pytest.mark.parametrize("waves", ["1", "2"])
 @pytest.mark.parametrize("feats", [128, 256])
-def test_spmm_both_task_forms(oracle, golden, gpu, feats, waves, monkeypatch):
-    """Each task form whatever the launch would pick (TCC_SPMM_TASK_WAVES): one wave per task, or
+def test_spmm_both_task_forms(oracle, golden, gpu, feats, waves, launch_overrides):
+    """Each task form whatever the launch would pick (forced through setSpmmLaunchOverrides): one wave per task, or
     the task's panels shared by two waves whose accumulators wave 0 adds in wave order. On the
     split and bucket-edge golden cases and on c2: Y within tolerance of the oracle, counters back to
     zero (checked by _run), and a repeated launch bitwise identical."""
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", waves)
+    launch_overrides(task_waves=int(waves))
     for case in ("empty_all", "single", "tail_33", "long_shared", "panels_384", "panels_385",
                  "split_mixed", "split_two"):
         rows, cols = (int(x) for x in golden[f"{case}/dims"])
@@ -257,6 +257,76 @@ def test_concurrent_launches_with_separate_workspaces(oracle, gpu, feats):
     assert_close(y_serial, y_ref, f"concurrent F{feats}")
 
 
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_float_aligned_output_and_partials(oracle, gpu, feats):
+    """Y and the workspace partials need only be float-aligned, as in the reference (it stores single
+    floats, src/kernel/spmm_kernel.cuh:236-245): bases 4, 8 and 12 bytes past a 16-byte boundary, for
+    either buffer or both, on a plan with split SWs, give Y bitwise equal to the aligned launch, leave
+    the floats around Y untouched and the counters at zero; the allocation-free entry point takes
+    such a Y as well."""
+    import torch
+    from tcc_spmm_amd.device import SpmmWorkspace, launch_spmm_int8, launch_spmm_int8_noalloc
+    c2 = _split_heavy_csr()
+    fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
+    assert fmt.partial_count > 0
+    x = features(c2.cols, feats, seed=79)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    dm, y_aligned = _run(fmt, packed, scale, feats, gpu)
+    ny, npart = c2.rows * feats, dm.partials.numel()
+    for oy, op in ((1, 1), (2, 2), (3, 3), (0, 1), (2, 0), (3, 2)):
+        ybuf = torch.full((ny + 8,), float("nan"), device=gpu)
+        pbuf = torch.full((npart + 8,), float("nan"), device=gpu)
+        assert ybuf.data_ptr() % 16 == 0 and pbuf.data_ptr() % 16 == 0
+        y, part = ybuf[oy:oy + ny], pbuf[op:op + npart]
+        launch_spmm_int8(dm.view, packed, scale, y, c2.rows, c2.cols, feats,
+                         SpmmWorkspace(part, dm.counters))
+        torch.cuda.synchronize()
+        assert int(dm.counters.abs().sum()) == 0, (oy, op)
+        got = ybuf.cpu().numpy()
+        assert np.array_equal(got[oy:oy + ny].view(np.uint32),
+                              y_aligned.ravel().view(np.uint32)), (feats, oy, op)
+        assert np.isnan(got[:oy]).all() and np.isnan(got[oy + ny:]).all(), (oy, op)
+    ybuf = torch.full((ny + 8,), float("nan"), device=gpu)
+    launch_spmm_int8_noalloc(dm.view, packed, scale, ybuf[1:1 + ny], c2.rows, c2.cols, feats,
+                             fmt.partial_count)
+    torch.cuda.synchronize()
+    assert np.array_equal(ybuf[1:1 + ny].cpu().numpy().view(np.uint32),
+                          y_aligned.ravel().view(np.uint32))
+    y_ref = oracle.sw32(c2.rows, c2.cols, *c2.views()).spmm_f64(pk, sc)
+    assert_close(y_aligned, y_ref, f"float-aligned F{feats}")
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_view_over_a_later_part_of_the_task_list(gpu, feats, launch_overrides):
+    """A view whose task list starts at a later SW (valid input: the reference maps blockIdx to a
+    task directly) computes exactly those SWs' rows, bitwise as the whole launch does, and leaves
+    the earlier rows untouched. On c2 the XCD ranges are panel-balanced, measured from the first
+    task's begin."""
+    import torch
+    from tcc_spmm_amd._lib import DeviceView
+    from tcc_spmm_amd.device import TorchDeviceMatrix, launch_spmm_int8
+    launch_overrides(task_waves=1)
+    csr = T.synth_csr("c2")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    tasks = fmt.tasks
+    # The first task of an SW a third of the way in (every chunk of a split SW stays in the view).
+    first_of_sw = np.flatnonzero(np.diff(tasks["sw"].astype(np.int64), prepend=-1) != 0)
+    cut = int(first_of_sw[first_of_sw.size // 3])
+    sw0 = int(tasks["sw"][cut])
+    packed, scale, *_ = gpu_prepare(features(csr.cols, feats, seed=81), gpu)
+    dm, y_full = _run(fmt, packed, scale, feats, gpu)
+    view = DeviceView.from_buffer_copy(dm.view)
+    view.tasks = dm.view.tasks + cut * tasks.dtype.itemsize
+    view.taskCount = tasks.size - cut
+    y = torch.full((csr.rows, feats), float("nan"), device=gpu)
+    launch_spmm_int8(view, packed, scale, y, csr.rows, csr.cols, feats, dm.workspace())
+    torch.cuda.synchronize()
+    assert int(dm.counters.abs().sum()) == 0
+    got = y.cpu().numpy()
+    assert np.isnan(got[:sw0 * 32]).all()
+    assert np.array_equal(got[sw0 * 32:].view(np.uint32), y_full[sw0 * 32:].view(np.uint32))
+
+
 def test_native_device_matrix_matches_torch_upload(gpu):
     import torch
     from tcc_spmm_amd.device import NativeDeviceMatrix
@@ -363,14 +433,14 @@ def test_spmm_huge_a_values_stay_finite(oracle, gpu, feats):
 
 
 @pytest.mark.parametrize("feats", [128, 256])
-def test_spmm_u16_aligned_packed_x(oracle, golden, gpu, feats, monkeypatch):
+def test_spmm_u16_aligned_packed_x(oracle, golden, gpu, feats, launch_overrides):
     """packedX need only be u16-aligned, as in the reference (include/format/int8_features.cuh:11-13):
     packed features placed 2, 6 and 14 bytes past a 16-byte boundary give Y bitwise equal to the
     aligned launch; an odd address raises invalid_argument before any launch. (The u16 instance
     runs one wave per task, so the aligned launch is held to one wave as well.)"""
     import torch
     from tcc_spmm_amd.device import TorchDeviceMatrix
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", "1")
+    launch_overrides(task_waves=1)
     for case in ("tail_33", "all_masks", "split_mixed", "random_3"):
         rows, cols = (int(v) for v in golden[f"{case}/dims"])
         off, src, val = (golden[f"{case}/csr_offsets"], golden[f"{case}/csr_sources"],
@@ -416,11 +486,11 @@ def test_quantize_subnormal_and_huge_rows_bit_exact(oracle, gpu):
 
 
 @pytest.mark.parametrize("feats", [128, 256])
-def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
+def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, launch_overrides):
     """The 64-bit-addressing kernel instance (taken when packed X exceeds 32-bit byte offsets) gives
     the same Y as the buffer-addressed one (both at one wave per task, the wide instance's only
     form)."""
-    monkeypatch.setenv("TCC_SPMM_TASK_WAVES", "1")
+    launch_overrides(task_waves=1)
     for case in ("single", "tail_33", "all_masks", "long_shared", "panels_385", "split_mixed",
                  "split_two", "random_3"):
         rows, cols = (int(x) for x in golden[f"{case}/dims"])
@@ -430,9 +500,9 @@ def test_spmm_wide_addressing_instance(oracle, golden, gpu, feats, monkeypatch):
         x = features(cols, feats, seed=rows + 3 * cols, stddev=2.0)
         packed, scale, _, sc, pk = gpu_prepare(x, gpu)
         _, y_narrow = _run(fmt, packed, scale, feats, gpu)
-        monkeypatch.setenv("TCC_SPMM_FORCE_WIDE", "1")
+        launch_overrides(task_waves=1, force_wide=True)
         _, y_wide = _run(fmt, packed, scale, feats, gpu)
-        monkeypatch.delenv("TCC_SPMM_FORCE_WIDE")
+        launch_overrides(task_waves=1)
         assert np.array_equal(y_wide.view(np.uint32), y_narrow.view(np.uint32)), case
         y_ref = oracle.sw32(rows, cols, off, src, val).spmm_f64(pk, sc)
         assert_close(y_wide, y_ref, f"{case} F{feats} wide")

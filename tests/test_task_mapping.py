@@ -74,14 +74,14 @@ def _equal(count, x):
 def _bounds(begin, panels_total):
     count = len(begin)
     first = [int(begin[t]) if t < count else panels_total for t in (_equal(count, k) for k in range(9))]
-    panels = first[8]
+    panels = first[8] - first[0]
     balanced = max(first[k + 1] - first[k] for k in range(8)) * 8 * 100 > panels * 103
     reach = _spare(count) // 2
 
     def bound(k):
         if k in (0, 8) or not balanced:
             return _equal(count, k)
-        lower = int(np.searchsorted(begin, panels * k // 8, side="left"))
+        lower = int(np.searchsorted(begin, first[0] + panels * k // 8, side="left"))
         eq = _equal(count, k)
         return min(max(lower, eq - reach if eq > reach else 0), eq + reach)
 
@@ -155,3 +155,22 @@ def test_probe_search_is_a_lower_bound():
             for target in targets:
                 want = int(np.searchsorted(begin, target, side="left"))
                 assert _panel_bound(begin, n, target) == want, (kind, n, target)
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c5"])
+def test_offset_task_list_maps_like_the_whole(cfg):
+    """A view over a later part of a plan's task list (valid input: the reference maps blockIdx to a
+    task directly) starts past panel 0. The ranges are measured from its first task's begin, so the
+    boundaries of a shifted list are those of the same list starting at 0, and every task is still
+    covered once."""
+    csr = T.synth_csr(cfg)
+    tasks = T.convert_csr_to_sw32(csr.rows, csr.cols, csr).tasks
+    begin = tasks["begin"].astype(np.int64)
+    end = int(tasks["end"][-1])
+    cut = int(np.searchsorted(begin, begin[begin.size // 3], side="left"))
+    sub = begin[cut:]
+    base = _bounds(sub - sub[0], end - int(sub[0]))
+    assert base[0]  # skewed enough to take the panel-balanced ranges
+    for shift in (int(sub[0]), int(sub[0]) + 12345):
+        assert _bounds(sub - sub[0] + shift, end - int(sub[0]) + shift) == base
+        assert _covered_once(sub - sub[0] + shift, end - int(sub[0]) + shift) == (True, True)

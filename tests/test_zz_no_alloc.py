@@ -41,10 +41,13 @@ def test_noalloc_matches_workspace_entry_on_two_calls(oracle, gpu):
         dm.partials.fill_(float("nan"))
         dm.spmm(packed, scale, y_ws)
         outs = []
-        for _ in range(2):  # the repeat starts from the counters and tiles this call leaves
+        for it in range(2):  # the repeat starts from the counters and tiles this call leaves
             y = torch.full((csr.rows, feats), float("nan"), device=gpu)
-            launch_spmm_int8_noalloc(dm.view, packed, scale, y, csr.rows, csr.cols, feats,
-                                     fmt.partial_count)
+            if it == 0:
+                launch_spmm_int8_noalloc(dm.view, packed, scale, y, csr.rows, csr.cols, feats,
+                                         fmt.partial_count)
+            else:  # the matrix object passes its own plan's partial count
+                dm.spmm_noalloc(packed, scale, y)
             outs.append(y)
         torch.cuda.synchronize()
         want = y_ws.cpu().numpy()
