@@ -224,15 +224,7 @@ def main() -> None:
     ap.add_argument("--no-model", action="store_true", help="skip the L2 traffic model")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (counter calibration)")
-    ap.add_argument("--probe-gather", action="store_true",
-                    help="only run model/gather_probe (random-request rate beyond L2) and print it")
     args = ap.parse_args()
-    if args.probe_gather:
-        import subprocess
-        import model
-        if not model.PROBE.exists():
-            model.build()
-        sys.exit(subprocess.run([str(model.PROBE)]).returncode)
     if args.calibrate_copy:
         import torch
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")

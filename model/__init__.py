@@ -12,9 +12,10 @@ every line an XCD touches is fetched once, whatever the schedule within that XCD
 
     python -m model c3          # all three policies at F = 128 and 256, as JSON
 
-The time side comes from gather_probe.hip (`bench.py --probe-gather`): on MI355X the memory system
-serves a fixed number of random requests per second beyond L2 (about 50-55 G/s), whether they are 32,
-64 or 128 bytes long, so a launch's beyond-L2 request count divided by that rate bounds its time.
+The time side comes from a random-gather probe measured on MI355X (profiles/gather_probe_rates.md):
+the memory system serves a fixed number of random requests per second beyond L2 (about 50-55 G/s),
+whether they are 32, 64 or 128 bytes long, so a launch's beyond-L2 request count divided by that rate
+bounds its time.
 """
 from __future__ import annotations
 
@@ -52,9 +53,6 @@ def build() -> None:
     res = subprocess.run(["make", "-s", "-C", str(HERE)], capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"model build failed:\n{res.stdout}\n{res.stderr}")
-
-
-PROBE = HERE / "_build" / "gather_probe"
 
 
 def _lib():
