@@ -304,10 +304,16 @@ __device__ __forceinline__ void scaleBlock(unsigned d0, unsigned d1, unsigned d2
     for (unsigned i = 0; i < 4; ++i) q[i] = c[i] * mant[i];
 }
 
-// TF32-round two values and pack them as f16 (round toward zero after adding half an ulp).
+// TF32-round two values and pack them as f16 (round toward zero after adding half an ulp). Both
+// half-ulp additions are one 64-bit add on the pair's patterns: no carry crosses from the low value
+// into the high one, since a finite FP32 pattern plus 0x1000 stays below 2^32 (only patterns at or
+// above 0xFFFFF000, negative NaNs, would carry). One v_lshl_add_u64 instead of two v_add_u32.
 __device__ __forceinline__ f16x2 roundPack(float a, float b) {
-    return __builtin_amdgcn_cvt_pkrtz(__uint_as_float(__float_as_uint(a) + 0x1000u),
-                                      __uint_as_float(__float_as_uint(b) + 0x1000u));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const unsigned long long both =
+        __builtin_bit_cast(unsigned long long, f32x2{a, b}) + 0x0000100000001000ull;
+    const f32x2 r = __builtin_bit_cast(f32x2, both);
+    return __builtin_amdgcn_cvt_pkrtz(r[0], r[1]);
 }
 
 // LDS handoff between the lanes of the workgroup's single wave: the wave's LDS operations execute
