@@ -293,15 +293,10 @@ __device__ __forceinline__ void loadStage(const Ld& ld, const Meta& m, unsigned 
 template <unsigned B>
 __device__ __forceinline__ void scaleBlock(unsigned d0, unsigned d1, unsigned d2, unsigned d3,
                                            const f32x4& mant, float (&q)[4]) {
-    float c[4];
-    asm("v_cvt_f32_i32_sdwa %0, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%5) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
-        "v_cvt_f32_i32_sdwa %2, sext(%6) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8\n\t"
-        "v_cvt_f32_i32_sdwa %3, sext(%7) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%c8"
-        : "=v"(c[0]), "=v"(c[1]), "=v"(c[2]), "=v"(c[3])
-        : "v"(d0), "v"(d1), "v"(d2), "v"(d3), "i"(B));
+    const unsigned d[4] = {d0, d1, d2, d3};
 #pragma unroll
-    for (unsigned i = 0; i < 4; ++i) q[i] = c[i] * mant[i];
+    for (unsigned i = 0; i < 4; ++i)
+        q[i] = float(static_cast<signed char>(d[i] >> (8 * B))) * mant[i];
 }
 
 // TF32-round two values and pack them as f16 (round toward zero after adding half an ulp). Both
@@ -361,29 +356,41 @@ struct LaneMh {
     unsigned m, h;
 };
 
+// Lanes whose value is a normal f16 (class bits 3 and 8: -normal, +normal), as a wave mask. The
+// comparison writes the mask straight into an SGPR pair; through the class builtin the compiler
+// moved the result through a VGPR and compared it again.
+__device__ __forceinline__ std::uint64_t normalF16(_Float16 v) {
+    std::uint64_t mask;
+    asm("v_cmp_class_f16_e64 %0, %1, %2" : "=s"(mask) : "v"(v), "v"(0x108u));
+    return mask;
+}
+
 template <bool Wide, unsigned G, unsigned S>
 __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups, unsigned lane,
                                                 const Lds& lds, f32x16 (&acc)[4 * S], unsigned keep,
                                                 LaneMh mh) {
     const int e = __builtin_amdgcn_frexp_expf(s.scale);
-    const bool scaleNormal = e > -126;
-    bool exact = true;
+    // Lanes whose slot's scale is normal (the mantissa trick needs it), as a wave mask.
+    const std::uint64_t scaleNormal = __builtin_amdgcn_ballot_w64(e > -126);
+    std::uint64_t inexact = 0; // lanes with an entry that has no exact f16 a'
     constexpr unsigned kCount = G < 4 ? 1 : 4;
-    float ap[kCount];
+    _Float16 ap[kCount];
 #pragma unroll
     for (unsigned j = 0; j < kCount; ++j) {
         const float at = stageTf32<Wide>(s, j);
-        ap[j] = __builtin_amdgcn_ldexpf(at, e + kShift);
-        // f16 normal range [2^-14, 2^16): biased FP32 exponent 113..142.
-        exact = exact & ((at == 0.0f) |
-                         ((((__float_as_uint(ap[j]) >> 23) & 0xFFu) - 113u <= 29u) & scaleNormal));
+        // a' has at most eleven significant bits, so it is exact in f16 exactly when its
+        // conversion is a normal f16: [2^-14, 65504]; larger values convert to inf, smaller ones
+        // to subnormals or zero. Masks of plain comparisons combine as scalar operations.
+        ap[j] = static_cast<_Float16>(__builtin_amdgcn_ldexpf(at, e + kShift));
+        const std::uint64_t nonzero = __builtin_amdgcn_ballot_w64(at != 0.0f);
+        inexact |= nonzero & ~(normalF16(ap[j]) & scaleNormal);
     }
     // A panel without exact f16 operands still runs its MFMAs (straight-line accumulators), on an
     // all-zero table; the FP32 pass adds it later.
-    const bool useF16 = __builtin_amdgcn_ballot_w64(!exact) == 0;
+    const bool useF16 = inexact == 0;
 #pragma unroll
     for (unsigned j = 0; j < kCount; ++j)
-        lds.table16[64 * (G < 4 ? G : j) + lane] = static_cast<_Float16>(useF16 ? ap[j] : 0.0f);
+        lds.table16[64 * (G < 4 ? G : j) + lane] = useF16 ? ap[j] : static_cast<_Float16>(0.0f);
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
@@ -394,23 +401,38 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
     const unsigned m = mh.m, h = mh.h;
     const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
     const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
+    // The S x 4 blocks are dequantized one ahead of their MFMAs: block i + 1's conversions run
+    // between block i's last pack and its MFMA, so the MFMA's operand was written a dozen VALU
+    // instructions before it is read and needs no wait states.
+    unsigned d[S][4];
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) {
         const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile + 64 * k) + m;
-        const unsigned d0 = xw[(4 * h + 0) * 32], d1 = xw[(4 * h + 1) * 32];
-        const unsigned d2 = xw[(4 * h + 2) * 32], d3 = xw[(4 * h + 3) * 32];
-        auto block = [&](auto blk) {
-            constexpr unsigned B = decltype(blk)::value;
-            float q[4];
-            scaleBlock<B>(d0, d1, d2, d3, mant, q);
-            const f16x4 av = __builtin_bit_cast(
-                f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
-            acc[4 * k + B] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + B], 0, 0, 0);
-        };
-        block(std::integral_constant<unsigned, 0>{});
-        block(std::integral_constant<unsigned, 1>{});
-        block(std::integral_constant<unsigned, 2>{});
-        block(std::integral_constant<unsigned, 3>{});
+#pragma unroll
+        for (unsigned i = 0; i < 4; ++i) d[k][i] = xw[(4 * h + i) * 32];
+    }
+    auto dequant = [&](auto blk, unsigned k) {
+        constexpr unsigned B = decltype(blk)::value;
+        float q[4];
+        scaleBlock<B>(d[k][0], d[k][1], d[k][2], d[k][3], mant, q);
+        return __builtin_bit_cast(
+            f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
+    };
+    using I0 = std::integral_constant<unsigned, 0>;
+    using I1 = std::integral_constant<unsigned, 1>;
+    using I2 = std::integral_constant<unsigned, 2>;
+    using I3 = std::integral_constant<unsigned, 3>;
+    f16x4 av = dequant(I0{}, 0);
+#pragma unroll
+    for (unsigned k = 0; k < S; ++k) {
+        f16x4 nx = dequant(I1{}, k);
+        acc[4 * k + 0] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + 0], 0, 0, 0);
+        av = dequant(I2{}, k);
+        acc[4 * k + 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(nx, b, acc[4 * k + 1], 0, 0, 0);
+        nx = dequant(I3{}, k);
+        acc[4 * k + 2] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + 2], 0, 0, 0);
+        if (k + 1 < S) av = dequant(I0{}, k + 1);
+        acc[4 * k + 3] = __builtin_amdgcn_mfma_f32_32x32x8f16(nx, b, acc[4 * k + 3], 0, 0, 0);
     }
     waveSync();
     return useF16;
