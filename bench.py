@@ -24,9 +24,9 @@ X row, scale line and A-stream line it touches exactly once (unbounded L2), plus
 the hardware does; it matches the counters) and with optimal replacement (the fewest misses any policy
 could reach on this access order in a 4 MiB L2), and the launch's rate of beyond-L2 requests.
 
-cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c) over the whole workload, median
-of 5 runs on up to 16 threads (about 10 s of CPU work); plus a single-thread figure over a prefix of SWs
-(~5 s), scaled by panel share.
+cpu_baseline: the C oracle's multithreaded FP32 SpMM (oracle/tcc_oracle.c; AVX2 when the host has it)
+over the whole workload, median of 5 runs on up to 16 threads; plus a single-thread figure over a prefix
+of SWs (~5 s), scaled by panel share.
 """
 from __future__ import annotations
 
@@ -164,7 +164,10 @@ def run_workload(csr, fmt, features, seed, steps, warmup, dev):
 
 
 def cpu_baseline(csr, fmt, features, seed, single_budget_s=5.0):
-    """Oracle FP32 SpMM on the host (dequantization, TF32 operands, FP32 row-order accumulation).
+    """Oracle FP32 SpMM on the host (dequantization, TF32 operands, FP32 accumulation in SW slot
+    order). On a CPU with AVX2 and FMA it takes the oracle's vector path: each slot's X row is
+    unpacked, dequantized and TF32-rounded once, eight features per instruction, and every row of
+    the slot accumulates exact products with fused multiply-adds (Y bitwise the scalar path's).
 
     Multithreaded, over the whole workload: one warm-up over a prefix of SWs, then 5 runs over all
     SWs; the median is the figure. Threads: the host's cores up to 16, the CPU share of a one-GPU
@@ -190,9 +193,11 @@ def cpu_baseline(csr, fmt, features, seed, single_budget_s=5.0):
     def share(sw_end):
         return float(wo[sw_end] - wo[0]) / float(wo[-1] - wo[0])
 
+    vector = of.has_vector_path()
+
     def timed(sw_end, nthreads):
         t = time.time()
-        _, used = of.spmm_f32_mt(packed, sc, 0, sw_end, nthreads, y)
+        _, used = of.spmm_f32_mt(packed, sc, 0, sw_end, nthreads, y, vector=vector)
         return time.time() - t, used
 
     probe = min(n_sw, 2000)
@@ -206,7 +211,9 @@ def cpu_baseline(csr, fmt, features, seed, single_budget_s=5.0):
     ms_single = dt1 * 1e3 / share(sample1)
     return {"value": round(ms_full, 3), "unit": "ms/SpMM", "cores": int(used), "kind": "port",
             "sample": f"the whole workload ({n_sw} SWs, all panels), median of 5 runs after a "
-                      f"warm-up; FP32 TF32-operand SpMM from oracle/tcc_oracle.c with {used} threads",
+                      f"warm-up; FP32 TF32-operand SpMM from oracle/tcc_oracle.c "
+                      f"({'AVX2: each slot row dequantized once, eight lanes per instruction' if vector else 'scalar C'}"
+                      f", SW slot order) with {used} threads",
             "runs_ms": [round(r[0] * 1e3, 1) for r in runs],
             "single_thread": {"value": round(ms_single, 1), "unit": "ms/SpMM", "cores": 1,
                               "sample": f"first {sample1} SWs ({share(sample1):.1%} of panels), "

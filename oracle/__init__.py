@@ -126,6 +126,10 @@ class Oracle:
                                           C.c_void_p, C.c_void_p]
         so.orc_spmm_sw32_f32_mt.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p,
                                             C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_void_p]
+        so.orc_spmm_sw32_f32_mt_path.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p,
+                                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_int,
+                                                 C.c_void_p, C.c_int]
+        so.orc_cpu_has_avx2.restype = C.c_int
         so.orc_check_sw32_mt.argtypes = [C.POINTER(_OrcSw32), C.c_void_p, C.c_void_p, C.c_uint32,
                                          C.c_void_p, C.c_double, C.c_double, C.c_double, C.c_int,
                                          C.POINTER(_CheckStats), C.c_void_p]
@@ -289,16 +293,24 @@ class OracleFormat:
                                         feats, part.ctypes.data, y.ctypes.data)
         return y
 
-    def spmm_f32_mt(self, packed, scales, sw_begin, sw_end, threads, y=None):
+    def spmm_f32_mt(self, packed, scales, sw_begin, sw_end, threads, y=None, vector=False):
+        """FP32 SpMM of SWs [sw_begin, sw_end) on `threads` host threads; vector=True takes the
+        AVX2 path (bitwise the same Y; RuntimeError when the CPU lacks AVX2 and FMA)."""
         packed = np.ascontiguousarray(packed, np.int8)
         scales = np.ascontiguousarray(scales, np.float32)
         feats = packed.shape[1]
         if y is None:
             y = np.zeros((self.rows, feats), np.float32)
-        used = self._orc.so.orc_spmm_sw32_f32_mt(C.byref(self._f), packed.ctypes.data,
-                                                 scales.ctypes.data, feats, sw_begin, sw_end,
-                                                 threads, y.ctypes.data)
+        used = self._orc.so.orc_spmm_sw32_f32_mt_path(C.byref(self._f), packed.ctypes.data,
+                                                      scales.ctypes.data, feats, sw_begin, sw_end,
+                                                      threads, y.ctypes.data, int(vector))
+        if used < 0:
+            raise RuntimeError("vector CPU path unavailable (needs AVX2 + FMA and features % 16 == 0)"
+                               if used == -1 else "CPU SpMM worker out of memory")
         return y, used
+
+    def has_vector_path(self) -> bool:
+        return bool(self._orc.so.orc_cpu_has_avx2())
 
 
 class RefFormat:

@@ -111,6 +111,12 @@ void orc_spmm_tasks_f32(const orc_sw32* f, const int8_t* packedX, const float* s
 int orc_spmm_sw32_f32_mt(const orc_sw32* f, const int8_t* packedX, const float* scales,
                          uint32_t features, uint32_t swBegin, uint32_t swEnd, int threads,
                          float* y);
+/* The same with vector = 0 (scalar, portable C) or 1 (AVX2 + FMA: bitwise the same Y; returns -1
+ * when the CPU lacks them or features % 16 != 0, -2 when a worker ran out of memory). */
+int orc_spmm_sw32_f32_mt_path(const orc_sw32* f, const int8_t* packedX, const float* scales,
+                              uint32_t features, uint32_t swBegin, uint32_t swEnd, int threads,
+                              float* y, int vector);
+int orc_cpu_has_avx2(void);
 
 #ifdef __cplusplus
 }

@@ -155,6 +155,32 @@ def test_spmm_matches_dense_brute_force(oracle, rows, cols, feats, density):
     assert_close(fmt.spmm_tasks_f32(pk, s), want, "tasks f32")
     y, _ = fmt.spmm_f32_mt(pk, s, 0, (rows + 31) // 32, 2)
     assert_close(y, want, "mt f32")
+    if fmt.has_vector_path():  # the CPU baseline's AVX2 path: bitwise the scalar path's Y
+        yv, _ = fmt.spmm_f32_mt(pk, s, 0, (rows + 31) // 32, 2, vector=True)
+        assert np.array_equal(yv.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_cpu_baseline_vector_path_is_bitwise_the_scalar_path(oracle, feats):
+    """The AVX2 path of the CPU baseline (per slot: byte-shuffle unpack, eight conversions, scale and
+    TF32 rounding per instruction, fused multiply-adds of exact products) gives Y bitwise equal to
+    the portable scalar path, on c1 with both widths and 1 or 3 threads; the scalar path is pinned
+    by the brute-force test above."""
+    of = None
+    csr = T.synth_csr("c1")
+    of = oracle.sw32(csr.rows, csr.cols, *csr.views())
+    if not of.has_vector_path():
+        pytest.skip("this CPU has no AVX2 + FMA")
+    x = T.synth_features(csr.cols, feats, 5)
+    q, s = oracle.quantize(x)
+    pk = oracle.pack16(q)
+    n_sw = (csr.rows + 31) // 32
+    y0, _ = of.spmm_f32_mt(pk, s, 0, n_sw, 3)
+    for threads in (1, 3):
+        y1, _ = of.spmm_f32_mt(pk, s, 0, n_sw, threads, vector=True)
+        assert np.array_equal(y1.view(np.uint32), y0.view(np.uint32))
+    with pytest.raises(RuntimeError):
+        of.spmm_f32_mt(pk[:, :8].copy(), s, 0, n_sw, 1, vector=True)  # features % 16 != 0
 
 
 def test_spmm_permutation_picks_rows_exactly(oracle):
