@@ -21,14 +21,18 @@
 //       partialIds order, and written to Y exactly once.
 //   merge_model map-lengths <F> <n>...
 //       the same for single reduction ranges of n tiles each (synthetic, distinct tile ids).
-//   merge_model run <plan> <threads> <launches> <workspaces> <seed> [relaxed]
+//   merge_model run <plan> <threads> <launches> <workspaces> <seed>
 //       the protocol on host threads: every split task of every workspace, in a shuffled order with
 //       random delays between the tile writes and the tickets, repeated for several launches on
 //       the same counters. Checks: exactly one merger per (SW, slice) and launch, counters at zero
 //       after every launch, and every merged Y element bitwise equal to the serial sum of the tile
 //       values in partialIds order (which also shows the merger saw every tile's final contents).
-//       `relaxed` plants a mistake for the ThreadSanitizer build to find: relaxed tickets and no
-//       acquire fence, so nothing orders the mergers' tile reads after the other tasks' writes.
+//   merge_model --plant <mistake> <mode> ...
+//       the same with a mistake planted in the model, to show that the checks catch it:
+//       relaxed       relaxed tickets and no acquire fence: nothing orders the mergers' tile reads
+//                     after the other tasks' writes (for the ThreadSanitizer build to report);
+//       batch-order   the tiles of a batch added last to first;
+//       ticket-limit  the ticket wraps at chunks instead of chunks - 1.
 //
 // Plan file (little-endian u32): magic 0x50434354, version 1, features, rows, taskCount,
 // reductionCount, partialIdCount, partialCount, then tasks [taskCount][7] (sw, begin, end,
@@ -51,6 +55,9 @@ namespace {
 
 constexpr std::uint32_t kNoPartial = 0xFFFFFFFFu;
 constexpr unsigned kWave = 64, kSlice = 128, kMergeBatch = 4;
+
+enum Plant { kNoPlant, kRelaxed, kBatchOrder, kTicketLimit };
+Plant gPlant = kNoPlant; // a mistake planted on purpose (--plant), to test the checks
 
 struct Task {
     std::uint32_t sw, begin, end, partial, mask, chunks, reduceFirst;
@@ -106,7 +113,8 @@ void walkMerge(const std::uint32_t* ids, std::uint32_t begin, std::uint32_t end,
             for (; i + kMergeBatch <= items; i += kMergeBatch) {
                 // The batch's loads are issued first and added afterwards, in order: per element
                 // the additions are those of the batch's tiles in increasing i.
-                for (unsigned u = 0; u < kMergeBatch; ++u) tile(readlane(i + u));
+                for (unsigned u = 0; u < kMergeBatch; ++u)
+                    tile(readlane(gPlant == kBatchOrder ? i + kMergeBatch - 1 - u : i + u));
             }
             for (; i < items; ++i) tile(readlane(i));
         }
@@ -237,8 +245,8 @@ std::uint32_t wrappingTicket(std::atomic<std::uint32_t>& c, std::uint32_t limit,
     return old;
 }
 
-void runTask(const Plan& p, Workspace& ws, const Task& task, unsigned launch, bool relaxed,
-             std::mt19937& rng) {
+void runTask(const Plan& p, Workspace& ws, const Task& task, unsigned launch, std::mt19937& rng) {
+    const bool relaxed = gPlant == kRelaxed;
     const unsigned F = p.features, slices = F / kSlice;
     // Partial tiles of the row groups in task.mask.
     for (unsigned rw = 0; rw < 4; ++rw) {
@@ -256,7 +264,8 @@ void runTask(const Plan& p, Workspace& ws, const Task& task, unsigned launch, bo
     bool last[2] = {false, false};
     for (unsigned k = 0; k < slices; ++k) {
         const std::uint32_t ticket =
-            wrappingTicket(ws.counters[std::size_t(task.sw) * slices + k], task.chunks - 1, relaxed);
+            wrappingTicket(ws.counters[std::size_t(task.sw) * slices + k],
+                           gPlant == kTicketLimit ? task.chunks : task.chunks - 1, relaxed);
         last[k] = ticket == task.chunks - 1;
     }
     for (unsigned k = 0; k < slices; ++k) {
@@ -285,7 +294,7 @@ void runTask(const Plan& p, Workspace& ws, const Task& task, unsigned launch, bo
 }
 
 int runPlan(const Plan& p, unsigned threads, unsigned launches, unsigned workspaces,
-            unsigned seed, bool relaxed) {
+            unsigned seed) {
     const unsigned F = p.features, slices = F / kSlice;
     std::uint32_t nSW = 0;
     std::vector<std::uint32_t> split; // indices of split tasks
@@ -317,7 +326,7 @@ int runPlan(const Plan& p, unsigned threads, unsigned launches, unsigned workspa
             pool.emplace_back([&, th] {
                 std::mt19937 rng(seed * 131u + launch * 977u + th);
                 for (std::size_t i; (i = next.fetch_add(1, std::memory_order_relaxed)) < work.size();)
-                    runTask(p, ws[work[i].first], p.tasks[work[i].second], launch, relaxed, rng);
+                    runTask(p, ws[work[i].first], p.tasks[work[i].second], launch, rng);
             });
         }
         for (auto& t : pool) t.join();
@@ -373,6 +382,14 @@ int runPlan(const Plan& p, unsigned threads, unsigned launches, unsigned workspa
 } // namespace
 
 int main(int argc, char** argv) {
+    if (argc >= 3 && std::strcmp(argv[1], "--plant") == 0) {
+        if (std::strcmp(argv[2], "relaxed") == 0) gPlant = kRelaxed;
+        else if (std::strcmp(argv[2], "batch-order") == 0) gPlant = kBatchOrder;
+        else if (std::strcmp(argv[2], "ticket-limit") == 0) gPlant = kTicketLimit;
+        else return 2;
+        argc -= 2;
+        argv += 2;
+    }
     if (argc >= 3 && std::strcmp(argv[1], "map") == 0) {
         Plan p;
         if (!readPlan(argv[2], p)) return 2;
@@ -388,11 +405,11 @@ int main(int argc, char** argv) {
     if (argc >= 7 && std::strcmp(argv[1], "run") == 0) {
         Plan p;
         if (!readPlan(argv[2], p)) return 2;
-        const bool relaxed = argc >= 8 && std::strcmp(argv[7], "relaxed") == 0;
         return runPlan(p, unsigned(std::atoi(argv[3])), unsigned(std::atoi(argv[4])),
-                       unsigned(std::atoi(argv[5])), unsigned(std::atoi(argv[6])), relaxed);
+                       unsigned(std::atoi(argv[5])), unsigned(std::atoi(argv[6])));
     }
-    std::fprintf(stderr, "usage: merge_model map <plan> | map-lengths <F> <n>... | "
-                         "run <plan> <threads> <launches> <workspaces> <seed> [relaxed]\n");
+    std::fprintf(stderr, "usage: merge_model [--plant relaxed|batch-order|ticket-limit] "
+                         "map <plan> | map-lengths <F> <n>... | "
+                         "run <plan> <threads> <launches> <workspaces> <seed>\n");
     return 2;
 }

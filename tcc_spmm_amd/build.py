@@ -124,8 +124,12 @@ def build_sanitized(verbose: bool = False) -> pathlib.Path:
 
         python -m tcc_spmm_amd.build --sanitize
         TCC_SPMM_LIB=tcc_spmm_amd/_san/libtcc_spmm.so TCC_ORACLE_LIB=oracle/_san/liboracle.so \
+        TCC_SANITIZER_RUN=1 \
         LD_PRELOAD=$(/opt/rocm/llvm/bin/clang -print-file-name=libclang_rt.asan-x86_64.so) \
         ASAN_OPTIONS=detect_leaks=0 python -m pytest tests -m "not gpu"
+
+    (TCC_SANITIZER_RUN makes the ThreadSanitizer tests of the merge model skip: their binaries cannot
+    run with ASan's runtime preloaded.)
     """
     SAN_DIR.mkdir(exist_ok=True)
     build()  # the ordinary objects, HIP ones included

@@ -115,6 +115,11 @@ def _tsan_env():
 
 
 def _tsan(*args):
+    import os
+    if os.environ.get("TCC_SANITIZER_RUN"):
+        # The AddressSanitizer run of this suite preloads ASan's runtime into every child process;
+        # a ThreadSanitizer binary cannot run beside it (and is a sanitizer run of its own).
+        pytest.skip("ThreadSanitizer binaries do not run inside the AddressSanitizer run")
     res = _run(MODEL_TSAN, *args, env=_tsan_env())
     if res.returncode != 0 and "unexpected memory mapping" in res.stderr:
         # Some kernels place mappings where this TSan runtime does not expect them; without
@@ -135,6 +140,19 @@ def test_tsan_reports_a_planted_relaxed_ticket(plans):
     """The planted mistake: relaxed tickets and no acquire fence leave the mergers' tile reads
     unordered after the other tasks' writes. The values still come out right on this host (its
     stores are ordered anyway), so only the race detector can tell; it must."""
-    res = _tsan("run", plans[("many", 128)], 8, 1, 1, 5, "relaxed")
+    res = _tsan("--plant", "relaxed", "run", plans[("many", 128)], 8, 1, 1, 5)
     assert res.returncode == 66, (res.returncode, res.stdout, res.stderr[-2000:])
     assert "WARNING: ThreadSanitizer: data race" in res.stderr
+
+
+@pytest.mark.parametrize("mistake,mode,want", [
+    ("batch-order", "map", "tiles not added in partialIds order"),
+    ("batch-order", "run", "merged value differs from the serial sum"),
+    ("ticket-limit", "run", "counter not back at zero"),
+])
+def test_checks_catch_planted_mistakes(plans, mistake, mode, want):
+    """Mistakes planted in the model (tiles of a batch added last to first; a ticket that wraps at
+    chunks instead of chunks - 1) fail the lane-map and protocol checks with the expected message."""
+    args = ("map", plans[("many", 256)]) if mode == "map" else ("run", plans[("many", 128)], 4, 1, 1, 3)
+    res = _run(MODEL, "--plant", mistake, *args)
+    assert res.returncode == 1 and want in res.stdout, (res.returncode, res.stdout, res.stderr[-500:])
