@@ -568,38 +568,47 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             pair = next;
             mFirst = pairPanel<0>(pair);
         }
+        if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
     } else {
-        const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last);
-        unsigned g1 = groupsAt(p1), g2 = groupsAt(p2);
-        // The loop expects m1's loads to be older than m2's (waits are counted in issue order).
-        Meta m1 = ld.meta8(p1, lane);
+        // F256: stage data two panels ahead, metadata four. Three stage buffers rotate through a loop
+        // unrolled by three: at the step of panel i they hold panels i, i + 1 and (loaded there)
+        // i + 2. Loads past the last panel repeat it (harmless, never computed).
+        Stage sc;
+        unsigned gc = 0;
+        const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last), p3 = min(lo + 3, last);
+        gb = groupsAt(p1);
+        loadStage<G, S>(ld, ld.meta8(p1, lane), gb, lane, sb);
+        unsigned g1 = groupsAt(p2), g2 = groupsAt(p3);
+        // The steps expect m1's loads to be older than m2's (waits are counted in issue order).
+        Meta m1 = ld.meta8(p2, lane);
         __builtin_amdgcn_sched_barrier(0);
-        Meta m2 = ld.meta8(p2, lane);
-        unsigned p = p2;
+        Meta m2 = ld.meta8(p3, lane);
+        unsigned p = p3;
+        auto step = [&](Stage& cur, unsigned gcur, Stage& ahead, unsigned& gahead,
+                        unsigned panel) __attribute__((always_inline)) {
+            gahead = g1;
+            loadStage<G, S>(ld, m1, gahead, lane, ahead);
+            p = min(p + 1, last);
+            m1 = m2;
+            g1 = g2;
+            g2 = groupsAt(p);
+            m2 = ld.meta8(p, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            flagRedo(w, panel, !computePanelF16<Ld::kWide, G, S>(cur, gcur, lane, w.lds, acc, w.keep, w.mh));
+        };
+        const unsigned triples = n / 3, rest = n - 3 * triples;
 #pragma unroll 1
-        for (unsigned k = 0; k < pairs; ++k) {
-            // Panels lo + 2k (in sa) and lo + 2k + 1; stage 2 one panel ahead, metadata two.
-            gb = g1;
-            loadStage<G, S>(ld, m1, gb, lane, sb);
-            p = min(p + 1, last);
-            m1 = m2;
-            g1 = g2;
-            g2 = groupsAt(p);
-            m2 = ld.meta8(p, lane);
-            __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
-            ga = g1;
-            loadStage<G, S>(ld, m1, ga, lane, sa);
-            p = min(p + 1, last);
-            m1 = m2;
-            g1 = g2;
-            g2 = groupsAt(p);
-            m2 = ld.meta8(p, lane);
-            __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
+        for (unsigned k = 0; k < triples; ++k) {
+            step(sa, ga, sc, gc, lo + 3 * k);
+            step(sb, gb, sa, ga, lo + 3 * k + 1);
+            step(sc, gc, sb, gb, lo + 3 * k + 2);
         }
+        if (rest >= 1)
+            flagRedo(w, lo + 3 * triples, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
+        if (rest == 2)
+            flagRedo(w, lo + 3 * triples + 1,
+                     !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
     }
-    if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
 }
 
 template <unsigned S, class Ld>
