@@ -35,8 +35,9 @@
 // is subnormal) takes an FP32 path with the same products: v_mfma_f32_32x32x2_f32 on tf32(a) / 2 and
 // the TF32 features. (Halving a value below 2^-125 rounds it, an error far below the tolerance.)
 //
-// The panels are walked by a software pipeline (metadata two panels ahead, in pairs of panels at
-// F128; A values and X one panel ahead) whose memory operations are identical on every path. F128
+// The panels are walked by a software pipeline (F128: metadata two panels ahead, in pairs of panels,
+// A values and X one panel ahead; F256: metadata four panels ahead, A values and X two) whose memory
+// operations are identical on every path. F128
 // runs four waves per SIMD (128 registers each, accumulators included), F256 two (196 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
@@ -523,7 +524,9 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 // F128 (S == 1) loads the metadata, sourceIds and scales of two panels with one instruction each, one
 // iteration ahead, and hands each panel its slots by DPP row shifts: per panel that is one and
 // a half vector memory instructions fewer (c3: 3.51 -> 3.39 ms). F256, at two waves per SIMD, keeps
-// one metadata load per panel two panels ahead (pairs cost it 0.5-2% in every form tried).
+// one metadata load per panel (pairs cost it 0.5-2% in every form tried) and keeps two panels of
+// gathers in flight: stage data two panels ahead, metadata four (1.2% faster than one panel ahead;
+// three ahead gained 0.2% for 16 more registers).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4 * S]) {
