@@ -624,7 +624,8 @@ __device__ __forceinline__ void walkTask(const Ld& ld, const unsigned* offsets, 
     unsigned keep;
     asm("v_mov_b32 %0, 0x807fffff" : "=v"(keep));
     LaneMh mh;
-    asm("v_and_b32 %0, 31, %2\n\tv_lshrrev_b32 %1, 5, %2" : "=v"(mh.m), "=v"(mh.h) : "v"(lane));
+    // %0 is written before %2 is read again: early-clobber, so it never shares the input's register.
+    asm("v_and_b32 %0, 31, %2\n\tv_lshrrev_b32 %1, 5, %2" : "=&v"(mh.m), "=v"(mh.h) : "v"(lane));
     TaskWalk w{offsets, begin, end, lane, lds, 0u, keep, mh};
     auto clipLo = [&](unsigned t) { return max(offsets[t], begin); };
     auto clipHi = [&](unsigned t) { return min(offsets[t], end); };
