@@ -223,3 +223,32 @@ def test_conversion_reports_reference_first_defect_within_sw(case, request):
         with pytest.raises(OracleError) as ref:
             RefFormat().convert(rows, cols, off, src, val)
         assert (ref.value.code, ref.value.message) == (1, case["message"])
+
+
+def test_host_builders_run_concurrently_from_several_threads():
+    """The format builders keep no state between calls (reference include/format/sw32.h, csr.h:
+    free functions): several host threads canonicalising and converting different matrices at once
+    (the ctypes calls release the interpreter lock) get exactly the arrays of serial calls."""
+    import concurrent.futures as cf
+    cases = []
+    for seed in range(6):
+        rng = np.random.default_rng(100 + seed)
+        rows, cols = 3000 + 97 * seed, 5000
+        per_row = [rng.integers(0, cols, int(rng.integers(0, 40))) for _ in range(rows)]
+        off = np.concatenate([[0], np.cumsum([len(c) for c in per_row])]).astype(np.uint32)
+        src = np.concatenate(per_row).astype(np.uint32)
+        val = rng.uniform(0.1, 1.0, src.size).astype(np.float32)
+        cases.append((rows, cols, off, src, val))
+
+    def build(case):
+        rows, cols, off, src, val = case
+        csr = T.make_canonical_csr(rows, cols, off, src, val)
+        fmt = T.convert_csr_to_sw32(rows, cols, csr)
+        return {k: np.array(v, copy=True) for k, v in fmt.arrays(copy=False).items()}
+
+    serial = [build(c) for c in cases]
+    with cf.ThreadPoolExecutor(max_workers=6) as pool:
+        for _ in range(2):
+            for want, got in zip(serial, pool.map(build, cases)):
+                for name in FIELDS:
+                    assert _same_bytes(got[name], want[name]), name

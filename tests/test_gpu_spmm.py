@@ -257,20 +257,30 @@ def test_concurrent_launches_with_separate_workspaces(oracle, gpu, feats):
     assert_close(y_serial, y_ref, f"concurrent F{feats}")
 
 
+@pytest.mark.parametrize("form", ["one wave", "two waves", "64-bit", "u16 packed X"])
 @pytest.mark.parametrize("feats", [128, 256])
-def test_spmm_float_aligned_output_and_partials(oracle, gpu, feats):
+def test_spmm_float_aligned_output_and_partials(oracle, gpu, feats, form, launch_overrides):
     """Y and the workspace partials need only be float-aligned, as in the reference (it stores single
     floats, src/kernel/spmm_kernel.cuh:236-245): bases 4, 8 and 12 bytes past a 16-byte boundary, for
     either buffer or both, on a plan with split SWs, give Y bitwise equal to the aligned launch, leave
     the floats around Y untouched and the counters at zero; the allocation-free entry point takes
-    such a Y as well."""
+    such a Y as well. Every kernel instance compiles its own float-wise path: one and two waves per
+    task, the 64-bit instance, and the u16 instance (packed X 2 bytes past a 16-byte boundary)."""
     import torch
     from tcc_spmm_amd.device import SpmmWorkspace, launch_spmm_int8, launch_spmm_int8_noalloc
+    launch_overrides(task_waves=2 if form == "two waves" else 1, force_wide=form == "64-bit")
     c2 = _split_heavy_csr()
     fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
     assert fmt.partial_count > 0
     x = features(c2.cols, feats, seed=79)
     packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    if form == "u16 packed X":
+        buf = torch.zeros(packed.numel() + 32, dtype=torch.int8, device=gpu)
+        base = (16 - buf.data_ptr() % 16) % 16
+        view = buf[base + 2: base + 2 + packed.numel()].view(packed.shape)
+        view.copy_(packed)
+        assert view.data_ptr() % 16 == 2
+        packed = view
     dm, y_aligned = _run(fmt, packed, scale, feats, gpu)
     ny, npart = c2.rows * feats, dm.partials.numel()
     for oy, op in ((1, 1), (2, 2), (3, 3), (0, 1), (2, 0), (3, 2)):
@@ -284,7 +294,7 @@ def test_spmm_float_aligned_output_and_partials(oracle, gpu, feats):
         assert int(dm.counters.abs().sum()) == 0, (oy, op)
         got = ybuf.cpu().numpy()
         assert np.array_equal(got[oy:oy + ny].view(np.uint32),
-                              y_aligned.ravel().view(np.uint32)), (feats, oy, op)
+                              y_aligned.ravel().view(np.uint32)), (feats, form, oy, op)
         assert np.isnan(got[:oy]).all() and np.isnan(got[oy + ny:]).all(), (oy, op)
     ybuf = torch.full((ny + 8,), float("nan"), device=gpu)
     launch_spmm_int8_noalloc(dm.view, packed, scale, ybuf[1:1 + ny], c2.rows, c2.cols, feats,
@@ -293,7 +303,7 @@ def test_spmm_float_aligned_output_and_partials(oracle, gpu, feats):
     assert np.array_equal(ybuf[1:1 + ny].cpu().numpy().view(np.uint32),
                           y_aligned.ravel().view(np.uint32))
     y_ref = oracle.sw32(c2.rows, c2.cols, *c2.views()).spmm_f64(pk, sc)
-    assert_close(y_aligned, y_ref, f"float-aligned F{feats}")
+    assert_close(y_aligned, y_ref, f"float-aligned F{feats} {form}")
 
 
 @pytest.mark.parametrize("feats", [128, 256])
@@ -325,6 +335,49 @@ def test_spmm_view_over_a_later_part_of_the_task_list(gpu, feats, launch_overrid
     got = y.cpu().numpy()
     assert np.isnan(got[:sw0 * 32]).all()
     assert np.array_equal(got[sw0 * 32:].view(np.uint32), y_full[sw0 * 32:].view(np.uint32))
+
+
+@pytest.mark.parametrize("feats", [128, 256])
+def test_launches_from_several_host_threads(gpu, feats):
+    """launchSpmmInt8 keeps no per-call host state beyond read-only launch choices (the reference's
+    free functions are callable from several host threads with distinct workspaces and streams): four
+    host threads, each with its own stream and workspace, launching three times at once (the ctypes
+    calls release the interpreter lock), give Y bitwise equal to a serial launch, and every counter
+    array ends at zero."""
+    import threading
+    import torch
+    from tcc_spmm_amd.device import TorchDeviceMatrix
+    c2 = _split_heavy_csr()
+    fmt = T.convert_csr_to_sw32(c2.rows, c2.cols, c2)
+    packed, scale, *_ = gpu_prepare(features(c2.cols, feats, seed=83), gpu)
+    _, y_serial = _run(fmt, packed, scale, feats, gpu)
+    dms = [TorchDeviceMatrix(fmt, feats, device=gpu) for _ in range(4)]
+    outs = [[torch.full((c2.rows, feats), float("nan"), device=gpu) for _ in range(3)] for _ in range(4)]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        try:
+            torch.cuda.set_device(gpu)
+            stream = torch.cuda.Stream(device=gpu)
+            with torch.cuda.stream(stream):
+                for y in outs[i]:
+                    dms[i].spmm(packed, scale, y, stream=stream)
+            stream.synchronize()
+        except Exception as e:  # reported below, in the test's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in range(4):
+        assert int(dms[i].counters.abs().sum()) == 0
+        for y in outs[i]:
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), y_serial.view(np.uint32)), i
 
 
 def test_native_device_matrix_matches_torch_upload(gpu):
