@@ -38,7 +38,7 @@
 // The panels are walked by a software pipeline (F128: metadata two panels ahead, in pairs of panels,
 // A values and X one panel ahead; F256: metadata four panels ahead, A values and X two) whose memory
 // operations are identical on every path. F128
-// runs four waves per SIMD (128 registers each, accumulators included), F256 two (196 registers).
+// runs four waves per SIMD (128 registers each, accumulators included), F256 two (218 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes, per slice, an agent-scope
