@@ -8,7 +8,8 @@
 //   the SW: four v_mfma_f32_32x32x8_f16 per panel and 128-feature slice (one per 32-feature block;
 //   M = features, N = the 32 rows, K = the panel's 8 slots) into 4 x 16 FP32 accumulators per
 //   slice. F256 runs both slices in the same wave, so the A side of a panel is loaded and built
-//   once. Plans with few tasks for the chip take two waves per task instead, each walking half the
+//   once, and takes its panels in pairs: four v_mfma_f32_32x32x16_f16 per pair and slice, K = the
+//   pair's 16 slots. Plans with few tasks for the chip take two waves per task instead, each walking half the
 //   panels, with the second wave's accumulators added by the first (runTask).
 //
 // Operands of one panel
@@ -20,6 +21,8 @@
 //   B (slots x rows): an LDS table [32 rows][8 slots] of f16 A values; lane l reads row l & 31,
 //   slots 4h..4h+3. Rows of row groups the panel's bucket does not touch hold 0.
 //   D: lane l holds row l & 31 and, per block, M indices 8i + 4h + j (register 4i + j).
+//   F256 pairs: both panels' X rows, mantissas and tables sit in two LDS areas, and each operand
+//   takes its four values from the first panel and then four from the second (K = 16).
 //
 // Exact TF32 products in f16. With the slot's scale written s = m * 2^e (m in [0.5, 1)),
 // x_hat = tf32(fp32(q * s)) = tf32(fp32(q * m)) * 2^e exactly whenever s is normal, and
@@ -68,6 +71,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __fp16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr unsigned kWave = 64;
 constexpr unsigned kSlice = 128;
@@ -321,10 +325,10 @@ __device__ __forceinline__ void waveSync() {
 }
 
 struct Lds {
-    _Float16* table16; // [32 rows][8 slots] a' (f16 path)
+    _Float16* table16; // [32 rows][2 halves][2 areas][4 slots] a' (f16 path; see tableIndex)
     float* table32;    // [32 rows][8 slots] tf32(a) / 2 (FP32 path)
-    u32x4* xtile;      // [S][8 slots][128 bytes] X rows of the panel, one block per slice
-    float* mant;       // [8 slots] scale mantissas of the panel
+    u32x4* xtile;      // [2 areas][S][8 slots][128 bytes] X rows of a panel, one block per slice
+    float* mant;       // [2 areas][8 slots] scale mantissas of a panel
     unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
                           // the FP32 path, in the order found (a task has <= 384 panels)
 };
@@ -366,10 +370,39 @@ __device__ __forceinline__ std::uint64_t normalF16(_Float16 v) {
     return mask;
 }
 
+__device__ __forceinline__ f16x8 join(f16x4 lo, f16x4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// A panel is computed in two parts. stagePanel writes its operands to LDS area 0 or 1: the f16 A
+// table, the X tiles and the scale mantissas. crunch reads them back, dequantizes the X blocks and
+// runs the MFMAs, over area 0 alone (one v_mfma_f32_32x32x8_f16 per 32-feature block) or over both
+// areas (one v_mfma_f32_32x32x16_f16 per block, K = the 16 slots of two panels: lane half h holds
+// k = 8h + j, j < 4 area 0's slot 4h + j and j >= 4 area 1's slot 4h + j - 4, in both operands, so
+// each MFMA adds both panels' products). F256 computes its panels in pairs: half the MFMAs, and
+// half the matrix-core time, of one MFMA per panel and block.
+//
+// Table layout: F128 (one area) [32 rows][8 slots]; F256 [32 rows][2 halves][2 areas][4 slots], so
+// that the entries of row m and slots 4h .. 4h + 3 are 8 contiguous bytes per area and 16 for both.
+// Either way they start at f16 index 4 (2m + h) * kAreas of area 0. Lane L writes slot L & 7 of row
+// 8g + (L >> 3) of row group g: F128 index 64g + L.
+template <unsigned S>
+__device__ __forceinline__ unsigned tableEntry(unsigned g, unsigned lane, unsigned area) {
+    if constexpr (S == 1) {
+        return 64 * g + lane;
+    } else {
+        const unsigned row = 8 * g + (lane >> 3), slot = lane & 7;
+        return ((row * 2 + (slot >> 2)) * 2 + area) * 4 + (slot & 3);
+    }
+}
+
+// Writes panel `s` of kind G to LDS area `area`. Per lane: slot lane & 7, row lane >> 3 of each
+// row group; kind G < 4 writes only row group G (the others hold 0 for the whole bucket). Returns
+// whether every entry of the panel has an exact f16 a' (wave-uniform); if not, its table is all
+// zero, so the panel contributes nothing here.
 template <bool Wide, unsigned G, unsigned S>
-__device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups, unsigned lane,
-                                                const Lds& lds, f32x16 (&acc)[4 * S], unsigned keep,
-                                                LaneMh mh) {
+__device__ __forceinline__ bool stagePanel(const Stage& s, unsigned lane, const Lds& lds, unsigned area,
+                                           unsigned keep) {
     const int e = __builtin_amdgcn_frexp_expf(s.scale);
     // Lanes whose slot's scale is normal (the mantissa trick needs it), as a wave mask.
     const std::uint64_t scaleNormal = __builtin_amdgcn_ballot_w64(e > -126);
@@ -391,51 +424,103 @@ __device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned groups,
     const bool useF16 = inexact == 0;
 #pragma unroll
     for (unsigned j = 0; j < kCount; ++j)
-        lds.table16[64 * (G < 4 ? G : j) + lane] = useF16 ? ap[j] : static_cast<_Float16>(0.0f);
+        lds.table16[tableEntry<S>(G < 4 ? G : j, lane, area)] =
+            useF16 ? ap[j] : static_cast<_Float16>(0.0f);
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
+    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * (S * area + k) + lane] = s.x[k];
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
     // stored as m * 2^-kXShift. For a subnormal scale the bits are not that, but such a panel's
     // table is all zero (scaleNormal above) and the FP32 pass computes it.
-    lds.mant[lane & 7] = shiftedMantissa(s.scale, keep);
+    lds.mant[8 * area + (lane & 7)] = shiftedMantissa(s.scale, keep);
+    return useF16;
+}
+
+// Dequantized block B (bytes B of the lane's four X dwords) of one area, as f16 x~ * 2^-kXShift.
+template <unsigned B>
+__device__ __forceinline__ f16x4 dequantBlock(const unsigned (&d)[4], const f32x4& mant) {
+    float q[4];
+    scaleBlock<B>(d[0], d[1], d[2], d[3], mant, q);
+    return __builtin_bit_cast(
+        f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
+}
+
+// The MFMAs of area 0 (Pair false) or of areas 0 and 1 (Pair true). The S x 4 blocks are
+// dequantized one ahead of their MFMAs: block i + 1's conversions run between block i's last pack
+// and its MFMA, so the MFMA's operand was written a dozen VALU instructions before it is read and
+// needs no wait states.
+template <unsigned S, bool Pair>
+__device__ __forceinline__ void crunch(const Lds& lds, f32x16 (&acc)[4 * S], LaneMh mh) {
+    constexpr unsigned kAreas = Pair ? 2 : 1;
     waveSync();
     const unsigned m = mh.m, h = mh.h;
-    const f32x4 mant = reinterpret_cast<const f32x4*>(lds.mant)[h];
-    const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[m * 2 + h];
-    // The S x 4 blocks are dequantized one ahead of their MFMAs: block i + 1's conversions run
-    // between block i's last pack and its MFMA, so the MFMA's operand was written a dozen VALU
-    // instructions before it is read and needs no wait states.
-    unsigned d[S][4];
+    f32x4 mant[kAreas];
+    unsigned d[kAreas][S][4];
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) {
-        const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile + 64 * k) + m;
+    for (unsigned r = 0; r < kAreas; ++r) {
+        mant[r] = reinterpret_cast<const f32x4*>(lds.mant + 8 * r)[h];
 #pragma unroll
-        for (unsigned i = 0; i < 4; ++i) d[k][i] = xw[(4 * h + i) * 32];
+        for (unsigned k = 0; k < S; ++k) {
+            const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile + 64 * (S * r + k)) + m;
+#pragma unroll
+            for (unsigned i = 0; i < 4; ++i) d[r][k][i] = xw[(4 * h + i) * 32];
+        }
     }
-    auto dequant = [&](auto blk, unsigned k) {
-        constexpr unsigned B = decltype(blk)::value;
-        float q[4];
-        scaleBlock<B>(d[k][0], d[k][1], d[k][2], d[k][3], mant, q);
-        return __builtin_bit_cast(
-            f16x4, __builtin_shufflevector(roundPack(q[0], q[1]), roundPack(q[2], q[3]), 0, 1, 2, 3));
-    };
     using I0 = std::integral_constant<unsigned, 0>;
     using I1 = std::integral_constant<unsigned, 1>;
     using I2 = std::integral_constant<unsigned, 2>;
     using I3 = std::integral_constant<unsigned, 3>;
-    f16x4 av = dequant(I0{}, 0);
+    if constexpr (Pair) {
+        const f16x8 b = reinterpret_cast<const f16x8*>(lds.table16)[m * 2 + h];
+        auto op = [&](auto blk, unsigned k) {
+            constexpr unsigned B = decltype(blk)::value;
+            return join(dequantBlock<B>(d[0][k], mant[0]), dequantBlock<B>(d[1][k], mant[1]));
+        };
+        auto mfma = [&](unsigned t, f16x8 x) {
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x, b, acc[t], 0, 0, 0);
+        };
+        f16x8 av = op(I0{}, 0);
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) {
-        f16x4 nx = dequant(I1{}, k);
-        acc[4 * k + 0] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + 0], 0, 0, 0);
-        av = dequant(I2{}, k);
-        acc[4 * k + 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(nx, b, acc[4 * k + 1], 0, 0, 0);
-        nx = dequant(I3{}, k);
-        acc[4 * k + 2] = __builtin_amdgcn_mfma_f32_32x32x8f16(av, b, acc[4 * k + 2], 0, 0, 0);
-        if (k + 1 < S) av = dequant(I0{}, k + 1);
-        acc[4 * k + 3] = __builtin_amdgcn_mfma_f32_32x32x8f16(nx, b, acc[4 * k + 3], 0, 0, 0);
+        for (unsigned k = 0; k < S; ++k) {
+            f16x8 nx = op(I1{}, k);
+            mfma(4 * k + 0, av);
+            av = op(I2{}, k);
+            mfma(4 * k + 1, nx);
+            nx = op(I3{}, k);
+            mfma(4 * k + 2, av);
+            if (k + 1 < S) av = op(I0{}, k + 1);
+            mfma(4 * k + 3, nx);
+        }
+    } else {
+        const f16x4 b = reinterpret_cast<const f16x4*>(lds.table16)[(m * 2 + h) * (S == 1 ? 1 : 2)];
+        auto op = [&](auto blk, unsigned k) {
+            constexpr unsigned B = decltype(blk)::value;
+            return dequantBlock<B>(d[0][k], mant[0]);
+        };
+        auto mfma = [&](unsigned t, f16x4 x) {
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8f16(x, b, acc[t], 0, 0, 0);
+        };
+        f16x4 av = op(I0{}, 0);
+#pragma unroll
+        for (unsigned k = 0; k < S; ++k) {
+            f16x4 nx = op(I1{}, k);
+            mfma(4 * k + 0, av);
+            av = op(I2{}, k);
+            mfma(4 * k + 1, nx);
+            nx = op(I3{}, k);
+            mfma(4 * k + 2, av);
+            if (k + 1 < S) av = op(I0{}, k + 1);
+            mfma(4 * k + 3, nx);
+        }
     }
     waveSync();
+}
+
+// One panel alone: staged in area 0 and computed.
+template <bool Wide, unsigned G, unsigned S>
+__device__ __forceinline__ bool computePanelF16(const Stage& s, unsigned lane, const Lds& lds,
+                                                f32x16 (&acc)[4 * S], unsigned keep, LaneMh mh) {
+    const bool useF16 = stagePanel<Wide, G, S>(s, lane, lds, 0, keep);
+    crunch<S, false>(lds, acc, mh);
     return useF16;
 }
 
@@ -526,17 +611,23 @@ __device__ __forceinline__ void flagRedo(TaskWalk& w, unsigned panel, bool redo)
 // a half vector memory instructions fewer (c3: 3.51 -> 3.39 ms). F256, at two waves per SIMD, keeps
 // one metadata load per panel (pairs cost it 0.5-2% in every form tried) and keeps two panels of
 // gathers in flight: stage data two panels ahead, metadata four (1.2% faster than one panel ahead;
-// three ahead gained 0.2% for 16 more registers).
+// three ahead gained 0.2% for 16 more registers), and computes its panels in pairs, K = 16 per MFMA
+// (c3: 5.92 -> 5.72 ms).
 template <unsigned G, unsigned S, class Ld>
 __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned lo,
                                            unsigned hi, f32x16 (&acc)[4 * S]) {
     if (lo >= hi) return;
     const unsigned n = hi - lo, lane = w.lane;
     if constexpr (G < 4) {
-        // The other row groups' table rows stay 0 for the whole bucket.
+        // The other row groups' table rows (64 entries each per area) stay 0 for the whole bucket.
 #pragma unroll
-        for (unsigned g = 0; g < 4; ++g)
-            if (g != G) w.lds.table16[64 * g + lane] = static_cast<_Float16>(0.0f);
+        for (unsigned g = 0; g < 4; ++g) {
+            if (g == G) continue;
+            if constexpr (S == 1)
+                w.lds.table16[64 * g + lane] = static_cast<_Float16>(0.0f);
+            else // both areas: 128 entries, two per lane
+                reinterpret_cast<f16x2*>(w.lds.table16)[64 * g + lane] = f16x2{0, 0};
+        }
     }
     BucketCursor cur{w.offsets, 5, w.offsets[6]};
     auto groupsAt = [&](unsigned p) { return G < 4 ? (1u << G) : cur.groups(p); };
@@ -561,21 +652,21 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             // is in order, so computing first would wait for loads issued only half an
             // iteration ago.
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
+            flagRedo(w, lo + 2 * k, !computePanelF16<Ld::kWide, G, S>(sa, lane, w.lds, acc, w.keep, w.mh));
             ga = groupsAt(min(lo + 2 * k + 2, last));
             loadStage<G, S, Ld, false>(ld, mSecond, ga, lane, sa);
             __builtin_amdgcn_sched_barrier(0);
             sb.scale = __uint_as_float(pairHalf<0>(__float_as_uint(sc)));
-            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
+            flagRedo(w, lo + 2 * k + 1, !computePanelF16<Ld::kWide, G, S>(sb, lane, w.lds, acc, w.keep, w.mh));
             sa.scale = __uint_as_float(pairHalf<1>(__float_as_uint(sc)));
             pair = next;
             mFirst = pairPanel<0>(pair);
         }
-        if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
+        if (n & 1) flagRedo(w, last, !computePanelF16<Ld::kWide, G, S>(sa, lane, w.lds, acc, w.keep, w.mh));
     } else {
-        // F256: stage data two panels ahead, metadata four. Three stage buffers rotate through a loop
-        // unrolled by three: at the step of panel i they hold panels i, i + 1 and (loaded there)
-        // i + 2. Loads past the last panel repeat it (harmless, never computed).
+        // F256: stage data two panels ahead, metadata four. Three stage buffers rotate: at the step
+        // of panel i they hold panels i, i + 1 and (loaded there) i + 2. Loads past the last panel
+        // repeat it (harmless, never computed).
         Stage sc;
         unsigned gc = 0;
         const unsigned p1 = min(lo + 1, last), p2 = min(lo + 2, last), p3 = min(lo + 3, last);
@@ -587,7 +678,9 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
         __builtin_amdgcn_sched_barrier(0);
         Meta m2 = ld.meta8(p3, lane);
         unsigned p = p3;
-        auto step = [&](Stage& cur, unsigned gcur, Stage& ahead, unsigned& gahead,
+        // Step of panel `panel` (in `cur`): the loads of panel + 2 into `ahead`, then the panel staged
+        // in area 0 (first of a pair) or staged in area 1 and the pair computed (second).
+        auto step = [&](auto second, Stage& cur, Stage& ahead, unsigned& gahead,
                         unsigned panel) __attribute__((always_inline)) {
             gahead = g1;
             loadStage<G, S>(ld, m1, gahead, lane, ahead);
@@ -597,20 +690,39 @@ __device__ __forceinline__ void walkPanels(const Ld& ld, TaskWalk& w, unsigned l
             g2 = groupsAt(p);
             m2 = ld.meta8(p, lane);
             __builtin_amdgcn_sched_barrier(0);
-            flagRedo(w, panel, !computePanelF16<Ld::kWide, G, S>(cur, gcur, lane, w.lds, acc, w.keep, w.mh));
+            constexpr bool kSecond = decltype(second)::value;
+            flagRedo(w, panel, !stagePanel<Ld::kWide, G, S>(cur, lane, w.lds, kSecond ? 1u : 0u, w.keep));
+            if constexpr (kSecond) crunch<S, true>(w.lds, acc, w.mh);
         };
-        const unsigned triples = n / 3, rest = n - 3 * triples;
+        using First = std::integral_constant<bool, false>;
+        using Second = std::integral_constant<bool, true>;
+        // Panels in pairs, in a loop unrolled by six (the period of both the pairs and the stage
+        // rotation), then the r < 6 panels left: their pairs by the same steps and a last panel
+        // without a partner alone, staged in area 0. (A loop that leaves after any panel, computing
+        // the unpaired one on its way out, made the register allocator spill the accumulators.)
+        const unsigned sixes = n / 6, r = n - 6 * sixes;
+        unsigned i = lo;
 #pragma unroll 1
-        for (unsigned k = 0; k < triples; ++k) {
-            step(sa, ga, sc, gc, lo + 3 * k);
-            step(sb, gb, sa, ga, lo + 3 * k + 1);
-            step(sc, gc, sb, gb, lo + 3 * k + 2);
+        for (unsigned k = 0; k < sixes; ++k, i += 6) {
+            step(First{}, sa, sc, gc, i);
+            step(Second{}, sb, sa, ga, i + 1);
+            step(First{}, sc, sb, gb, i + 2);
+            step(Second{}, sa, sc, gc, i + 3);
+            step(First{}, sb, sa, ga, i + 4);
+            step(Second{}, sc, sb, gb, i + 5);
         }
-        if (rest >= 1)
-            flagRedo(w, lo + 3 * triples, !computePanelF16<Ld::kWide, G, S>(sa, ga, lane, w.lds, acc, w.keep, w.mh));
-        if (rest == 2)
-            flagRedo(w, lo + 3 * triples + 1,
-                     !computePanelF16<Ld::kWide, G, S>(sb, gb, lane, w.lds, acc, w.keep, w.mh));
+        if (r >= 2) {
+            step(First{}, sa, sc, gc, i);
+            step(Second{}, sb, sa, ga, i + 1);
+        }
+        if (r >= 4) {
+            step(First{}, sc, sb, gb, i + 2);
+            step(Second{}, sa, sc, gc, i + 3);
+        }
+        if (r & 1) {
+            const Stage& odd = r == 1 ? sa : r == 3 ? sc : sb;
+            flagRedo(w, hi - 1, !computePanelF16<Ld::kWide, G, S>(odd, lane, w.lds, acc, w.keep, w.mh));
+        }
     }
 }
 
@@ -889,10 +1001,11 @@ __device__ __forceinline__ void mergeSlice(const KernelArgs& a, const Sw32Task& 
 template <unsigned Features, unsigned Addr, unsigned Waves = 1>
 __device__ __forceinline__ void runTask(const KernelArgs& a, unsigned taskIndex) {
     constexpr unsigned S = Features / kSlice;
-    __shared__ __align__(16) _Float16 table16[Waves][256];
+    constexpr unsigned kAreas = S == 1 ? 1 : 2; // F256 computes its panels in pairs
+    __shared__ __align__(16) _Float16 table16[Waves][256 * kAreas];
     __shared__ __align__(16) float table32[Waves][256];
-    __shared__ __align__(16) u32x4 xtile[Waves][64 * S];
-    __shared__ __align__(16) float mant[Waves][8];
+    __shared__ __align__(16) u32x4 xtile[Waves][kAreas * 64 * S];
+    __shared__ __align__(16) float mant[Waves][8 * kAreas];
     __shared__ unsigned short redo[Waves][384];
     __shared__ unsigned lastFlag[S];
     const unsigned wave = Waves == 1 ? 0u : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
