@@ -64,6 +64,12 @@
 #include <string>
 #include <type_traits>
 
+// A 4-byte load from a structured buffer (address = base + index x stride + offsets, range-checked
+// by index): the LLVM intrinsic behind the raw-buffer builtins, declared by its name since clang
+// has no builtin for the structured form.
+__device__ float structLoadF32(__amdgpu_buffer_rsrc_t rsrc, int index, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.f32");
+
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -173,10 +179,9 @@ struct Loader<kBuffer> {
                                                 0x7FFFFFF0, 0x00020000);
         meta = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<std::uint64_t*>(a.m.sourceMetadata + slot0), 0, 0x7FFFFFF0, 0x00020000);
-        vals = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.m.values + vbase), 0,
+        vals = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.m.values + vbase), 4,
                                                  0x7FFFFFF0, 0x00020000);
-        scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.scales), 0, a.cols * 4u,
-                                                   0x00020000);
+        scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.scales), 4, a.cols, 0x00020000);
         x = __builtin_amdgcn_make_buffer_rsrc(const_cast<std::int8_t*>(a.packedX), 0,
                                               a.cols << xShift, 0x00020000);
     }
@@ -191,18 +196,18 @@ struct Loader<kBuffer> {
         const auto md = __builtin_amdgcn_raw_buffer_load_b64(meta, 2 * off, 0, kNt);
         return {__builtin_amdgcn_raw_buffer_load_b32(ids, off, 0, kNt), md[0], md[1]};
     }
-    __device__ float scale(unsigned src) const {
-        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(scales, src * 4u, 0, 0));
-    }
-    // values[idx] when `present`, else 0 (an out-of-range offset reads 0).
+    // scales and values are structured buffers of 4-byte records, addressed by index (no shift) and
+    // range-checked by index: an index past the records reads 0.
+    __device__ float scale(unsigned src) const { return structLoadF32(scales, int(src), 0, 0, 0); }
+    // values[idx] when `present`, else 0.
     __device__ float value(unsigned idx, bool present) const {
-        const unsigned off = present ? (idx - vbase) * 4u : 0xFFFFFFFCu;
-        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vals, off, 0, kNt));
+        return structLoadF32(vals, int(present ? idx - vbase : 0xFFFFFFFFu), 0, 0, kNt);
     }
-    // 16-byte tile `lane & 7` of slice k of the packed X row of `src`.
+    // 16-byte tile `lane & 7` of slice k of the packed X row of `src`. The slice offset goes in the
+    // scalar offset, so both slices of a row share one per-lane offset (one VALU instruction fewer
+    // per F256 panel).
     __device__ u32x4 tile(unsigned src, unsigned lane, unsigned k) const {
-        return __builtin_amdgcn_raw_buffer_load_b128(x, (src << xShift) + 16 * (lane & 7) + kSlice * k,
-                                                     0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(x, (src << xShift) + 16 * (lane & 7), kSlice * k, 0);
     }
 };
 
@@ -327,7 +332,7 @@ __device__ __forceinline__ void waveSync() {
 struct Lds {
     _Float16* table16; // [32 rows][2 halves][2 areas][4 slots] a' (f16 path; see tableIndex)
     float* table32;    // [32 rows][8 slots] tf32(a) / 2 (FP32 path)
-    u32x4* xtile;      // [2 areas][S][8 slots][128 bytes] X rows of a panel, one block per slice
+    u32x4* xtile;      // [8 slots][blocks][128 bytes] X rows: block S * area + slice (xBlock)
     float* mant;       // [2 areas][8 slots] scale mantissas of a panel
     unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
                           // the FP32 path, in the order found (a task has <= 384 panels)
@@ -396,6 +401,17 @@ __device__ __forceinline__ unsigned tableEntry(unsigned g, unsigned lane, unsign
     }
 }
 
+// X tiles in LDS: [8 slots][blocks][128 bytes], block S * area + slice (F128: one block; F256: four,
+// two areas of two slices). Returns the 16-byte index of the first tile of (slot, block). A lane
+// reads its four slots 4h .. 4h + 3 of one block at 128 * blocks bytes apart; with four blocks the
+// even blocks' reads are 256-byte multiples from one base and the odd blocks' from that base + 128,
+// which two-address LDS reads with 256-byte offset units (ds_read2st64) reach.
+template <unsigned S>
+__device__ __forceinline__ unsigned xTile(unsigned slot, unsigned block) {
+    constexpr unsigned kBlocks = S == 1 ? 1 : 2 * S;
+    return (slot * kBlocks + block) * 8;
+}
+
 // Writes panel `s` of kind G to LDS area `area`. Per lane: slot lane & 7, row lane >> 3 of each
 // row group; kind G < 4 writes only row group G (the others hold 0 for the whole bucket). Returns
 // whether every entry of the panel has an exact f16 a' (wave-uniform); if not, its table is all
@@ -427,7 +443,7 @@ __device__ __forceinline__ bool stagePanel(const Stage& s, unsigned lane, const 
         lds.table16[tableEntry<S>(G < 4 ? G : j, lane, area)] =
             useF16 ? ap[j] : static_cast<_Float16>(0.0f);
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * (S * area + k) + lane] = s.x[k];
+    for (unsigned k = 0; k < S; ++k) lds.xtile[xTile<S>(lane >> 3, S * area + k) + (lane & 7)] = s.x[k];
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
     // stored as m * 2^-kXShift. For a subnormal scale the bits are not that, but such a panel's
     // table is all zero (scaleNormal above) and the FP32 pass computes it.
@@ -460,9 +476,9 @@ __device__ __forceinline__ void crunch(const Lds& lds, f32x16 (&acc)[4 * S], Lan
         mant[r] = reinterpret_cast<const f32x4*>(lds.mant + 8 * r)[h];
 #pragma unroll
         for (unsigned k = 0; k < S; ++k) {
-            const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile + 64 * (S * r + k)) + m;
+            const unsigned* xw = reinterpret_cast<const unsigned*>(lds.xtile) + m;
 #pragma unroll
-            for (unsigned i = 0; i < 4; ++i) d[r][k][i] = xw[(4 * h + i) * 32];
+            for (unsigned i = 0; i < 4; ++i) d[r][k][i] = xw[4 * xTile<S>(4 * h + i, S * r + k)];
         }
     }
     using I0 = std::integral_constant<unsigned, 0>;
@@ -534,7 +550,7 @@ __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups,
     for (unsigned g = 0; g < 4; ++g)
         lds.table32[64 * g + lane] = ((groups >> g) & 1u) ? 0.5f * stageTf32<Wide>(s, g) : 0.0f;
 #pragma unroll
-    for (unsigned k = 0; k < S; ++k) lds.xtile[64 * k + lane] = s.x[k];
+    for (unsigned k = 0; k < S; ++k) lds.xtile[xTile<S>(lane >> 3, k) + (lane & 7)] = s.x[k];
     waveSync();
     const unsigned m = lane & 31, h = lane >> 5;
 #pragma unroll
@@ -545,7 +561,7 @@ __device__ __forceinline__ void computePanelF32(const Stage& s, unsigned groups,
         const float b = lds.table32[m * 8 + slot];
 #pragma unroll
         for (unsigned k = 0; k < S; ++k) {
-            const unsigned d = (reinterpret_cast<const unsigned*>(lds.xtile + 64 * k) + m)[slot * 32];
+            const unsigned d = (reinterpret_cast<const unsigned*>(lds.xtile) + m)[4 * xTile<S>(slot, k)];
 #pragma unroll
             for (unsigned blk = 0; blk < 4; ++blk) {
                 const float x = roundTf32(float(int(d << (24 - 8 * blk)) >> 24) * sc);
