@@ -403,9 +403,9 @@ __device__ __forceinline__ unsigned tableEntry(unsigned g, unsigned lane, unsign
 
 // X tiles in LDS: [8 slots][blocks][128 bytes], block S * area + slice (F128: one block; F256: four,
 // two areas of two slices). Returns the 16-byte index of the first tile of (slot, block). A lane
-// reads its four slots 4h .. 4h + 3 of one block at 128 * blocks bytes apart; with four blocks the
-// even blocks' reads are 256-byte multiples from one base and the odd blocks' from that base + 128,
-// which two-address LDS reads with 256-byte offset units (ds_read2st64) reach.
+// reads dword m of slots 4h .. 4h + 3 of every block: at F256 its 16 reads of a pair lie within 2 KB
+// of its first one, so two base addresses 1 KB apart reach them all through the 8-bit dword offsets
+// of two-address LDS reads (with one block per 1 KB, as [block][slot], it took four).
 template <unsigned S>
 __device__ __forceinline__ unsigned xTile(unsigned slot, unsigned block) {
     constexpr unsigned kBlocks = S == 1 ? 1 : 2 * S;
