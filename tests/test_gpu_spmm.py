@@ -419,10 +419,15 @@ def _fallback_entries(csr, scales):
             | (scales[csr.source_ids] < np.float32(2.0 ** -126)))
 
 
-def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu):
+@pytest.mark.parametrize("waves", ["1", "2"])
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu, feats, waves, launch_overrides):
     """A values of 1e4, 1e-7 and 1e-30 and X rows scaled by 1e6, 1e-6 and into the subnormal range
     push some panels onto the FP32 path; Y must still match the oracle (summation-conditioned
-    bound: the rows mix terms across 40 orders of magnitude)."""
+    bound: the rows mix terms across 40 orders of magnitude). At F256 panels go in pairs through
+    one MFMA, so flagged panels sit in either place of a pair and beside unflagged ones, and walks
+    of every length modulo six end with and without an unpaired panel."""
+    launch_overrides(task_waves=int(waves))
     base = T.synth_csr("t3000_24_11")
     rng = np.random.default_rng(12)
     val = base.values.copy()
@@ -432,7 +437,7 @@ def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu):
     val[(pick >= 0.08) & (pick < 0.085)] *= np.float32(1e-30)
     csr = T.make_canonical_csr(base.rows, base.cols, base.row_offsets, base.source_ids, val)
     fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
-    x = features(csr.cols, 128, seed=21, stddev=1.0)
+    x = features(csr.cols, feats, seed=21, stddev=1.0)
     rows = rng.permutation(csr.cols)
     x[rows[:60]] *= np.float32(1e6)
     x[rows[60:120]] *= np.float32(1e-6)
@@ -442,7 +447,7 @@ def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu):
     check_features(oracle, x, q, sc, pk)
     flagged = _fallback_entries(csr, sc)
     assert 0.01 < flagged.mean() < 0.5, flagged.mean()
-    _, y = _run(fmt, packed, scale, 128, gpu)
+    _, y = _run(fmt, packed, scale, feats, gpu)
     assert np.isfinite(y).all()
     windows = np.arange(len(fmt.window_offsets) - 1, dtype=np.uint32)
     _check_windows(oracle, csr, fmt, y, pk, sc, windows, "extreme", conditioned=True)
