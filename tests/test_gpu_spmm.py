@@ -453,6 +453,62 @@ def test_spmm_fp32_path_for_extreme_magnitudes(oracle, gpu, feats, waves, launch
     _check_windows(oracle, csr, fmt, y, pk, sc, windows, "extreme", conditioned=True)
 
 
+def _walk_length_csr():
+    """14 SWs: SW i has i + 1 panels in the exclusive bucket of row group i % 4 (its last panel short of
+    a slot when i % 3 != 0) and (5 i) % 7 panels in the shared bucket of row groups {0, 1}; in SWs 4 to 7
+    one entry in 16 is 1e6 times larger, so some panels, in either place of an F256 pair, take the FP32
+    path."""
+    rng = np.random.default_rng(7)
+    nsw, cols = 14, 4096
+    rows = 32 * nsw
+    row_cols = [[] for _ in range(rows)]
+    row_vals = [[] for _ in range(rows)]
+    nxt = 0
+
+    def add(r, c, big):
+        v = float(rng.uniform(0.1, 1.0)) * float(rng.choice([-1.0, 1.0]))
+        row_cols[r].append(c)
+        row_vals[r].append(v * (1e6 if big and rng.random() < 1 / 16 else 1.0))
+
+    for i in range(nsw):
+        g, big = i % 4, 4 <= i < 8
+        for c in range(nxt, nxt + 8 * (i + 1) - i % 3):
+            add(32 * i + 8 * g + int(rng.integers(0, 8)), c, big)
+        nxt += 8 * (i + 1) - i % 3
+        for c in range(nxt, nxt + 8 * ((5 * i) % 7)):
+            add(32 * i + int(rng.integers(0, 8)), c, big)
+            add(32 * i + 8 + int(rng.integers(0, 8)), c, big)
+        nxt += 8 * ((5 * i) % 7)
+    off = np.zeros(rows + 1, np.uint32)
+    src, val = [], []
+    for r in range(rows):
+        order = np.argsort(row_cols[r], kind="stable")
+        src += [row_cols[r][j] for j in order]
+        val += [row_vals[r][j] for j in order]
+        off[r + 1] = len(src)
+    return T.make_canonical_csr(rows, cols, off, np.array(src, np.uint32), np.array(val, np.float32))
+
+
+@pytest.mark.parametrize("waves", ["1", "2"])
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_every_walk_length(oracle, gpu, feats, waves, launch_overrides):
+    """Exclusive walks of 1 to 14 panels in every row group and shared walks of 0 to 6: every length
+    modulo six of the F256 loop (panels in pairs, a loop of six, a last panel alone) and of the F128
+    loop (pairs of panels), in both task forms (the two-wave form halves each walk)."""
+    launch_overrides(task_waves=int(waves))
+    csr = _walk_length_csr()
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    per = np.diff(fmt.bucket_offsets.reshape(-1, 17).astype(np.int64)[:, 1:17], axis=1)
+    assert sorted(per[:, :4].max(axis=1).tolist()) == list(range(1, 15))
+    assert sorted(set(per[:, 4:].sum(axis=1).tolist())) == list(range(7))
+    x = features(csr.cols, feats, seed=31)
+    packed, scale, q, sc, pk = gpu_prepare(x, gpu)
+    assert _fallback_entries(csr, sc).any()
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    windows = np.arange(len(fmt.window_offsets) - 1, dtype=np.uint32)
+    _check_windows(oracle, csr, fmt, y, pk, sc, windows, "walk lengths")
+
+
 @pytest.mark.parametrize("feats", [128, 256])
 def test_spmm_huge_a_values_stay_finite(oracle, gpu, feats):
     """A values at and above 2^118 (where tf32(a) * 2^10 would overflow FP32) up to 3e38 and 2^127,
