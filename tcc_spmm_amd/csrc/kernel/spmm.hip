@@ -41,7 +41,7 @@
 // The panels are walked by a software pipeline (F128: metadata two panels ahead, in pairs of panels,
 // A values and X one panel ahead; F256: metadata four panels ahead, A values and X two) whose memory
 // operations are identical on every path. F128
-// runs four waves per SIMD (128 registers each, accumulators included), F256 two (218 registers).
+// runs four waves per SIMD (128 registers each, accumulators included), F256 two (248 registers).
 //
 // Split SWs (reference src/kernel/spmm_kernel.cuh:228-282): a split task stores its row groups of
 // `task.mask` as 8-row partial tiles [tile][8][F]; lane 0 then takes, per slice, an agent-scope
@@ -330,9 +330,9 @@ __device__ __forceinline__ void waveSync() {
 }
 
 struct Lds {
-    _Float16* table16; // [32 rows][2 halves][2 areas][4 slots] a' (f16 path; see tableIndex)
+    _Float16* table16; // a' (f16 path): F128 [32 rows][8 slots], F256 two areas (tableEntry)
     float* table32;    // [32 rows][8 slots] tf32(a) / 2 (FP32 path)
-    u32x4* xtile;      // [8 slots][blocks][128 bytes] X rows: block S * area + slice (xBlock)
+    u32x4* xtile;      // [8 slots][blocks][128 bytes] X rows: block S * area + slice (xTile)
     float* mant;       // [2 areas][8 slots] scale mantissas of a panel
     unsigned short* redo; // [384]: offsets (from the task's first panel) of the panels that need
                           // the FP32 path, in the order found (a task has <= 384 panels)
