@@ -419,21 +419,26 @@ __device__ __forceinline__ unsigned xTile(unsigned slot, unsigned block) {
 template <bool Wide, unsigned G, unsigned S>
 __device__ __forceinline__ bool stagePanel(const Stage& s, unsigned lane, const Lds& lds, unsigned area,
                                            unsigned keep) {
-    const int e = __builtin_amdgcn_frexp_expf(s.scale);
-    // Lanes whose slot's scale is normal (the mantissa trick needs it), as a wave mask.
-    const std::uint64_t scaleNormal = __builtin_amdgcn_ballot_w64(e > -126);
+    // 2^(e + kShift) for the slot's scale s = m * 2^e (m in [0.5, 1)): its exponent bits alone are
+    // 2^(e - 1). A zero or subnormal scale gives 0 and an infinite or NaN one inf, so that every
+    // nonzero entry of such a slot fails the check below and the panel takes the FP32 path (the
+    // mantissa trick needs a normal scale; there q x inf is inf or NaN, as in the reference).
+    const float pow2 = __builtin_amdgcn_ldexpf(__uint_as_float(__float_as_uint(s.scale) & 0x7F800000u),
+                                               kShift + 1);
     std::uint64_t inexact = 0; // lanes with an entry that has no exact f16 a'
     constexpr unsigned kCount = G < 4 ? 1 : 4;
     _Float16 ap[kCount];
 #pragma unroll
     for (unsigned j = 0; j < kCount; ++j) {
         const float at = stageTf32<Wide>(s, j);
-        // a' has at most eleven significant bits, so it is exact in f16 exactly when its
-        // conversion is a normal f16: [2^-14, 65504]; larger values convert to inf, smaller ones
-        // to subnormals or zero. Masks of plain comparisons combine as scalar operations.
-        ap[j] = static_cast<_Float16>(__builtin_amdgcn_ldexpf(at, e + kShift));
+        // a' = at x pow2 has at most eleven significant bits, so it is exact in f16 exactly when
+        // its conversion is a normal f16: [2^-14, 65504]; larger values (inf included) convert to
+        // inf, smaller ones to subnormals or zero. (A product that lands in that range is a normal
+        // FP32 value, so the multiply itself was exact.) Masks of comparisons combine as scalar
+        // operations.
+        ap[j] = static_cast<_Float16>(at * pow2);
         const std::uint64_t nonzero = __builtin_amdgcn_ballot_w64(at != 0.0f);
-        inexact |= nonzero & ~(normalF16(ap[j]) & scaleNormal);
+        inexact |= nonzero & ~normalF16(ap[j]);
     }
     // A panel without exact f16 operands still runs its MFMAs (straight-line accumulators), on an
     // all-zero table; the FP32 pass adds it later.
@@ -445,8 +450,8 @@ __device__ __forceinline__ bool stagePanel(const Stage& s, unsigned lane, const 
 #pragma unroll
     for (unsigned k = 0; k < S; ++k) lds.xtile[xTile<S>(lane >> 3, S * area + k) + (lane & 7)] = s.x[k];
     // Lane L holds slot L & 7's scale; lanes of half h read the mantissas of slots 4h .. 4h + 3,
-    // stored as m * 2^-kXShift. For a subnormal scale the bits are not that, but such a panel's
-    // table is all zero (scaleNormal above) and the FP32 pass computes it.
+    // stored as m * 2^-kXShift. For a scale that is not normal the bits are not that, but such a
+    // panel's table is all zero (pow2 above) and the FP32 pass computes it.
     lds.mant[8 * area + (lane & 7)] = shiftedMantissa(s.scale, keep);
     return useF16;
 }

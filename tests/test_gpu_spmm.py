@@ -509,6 +509,41 @@ def test_spmm_every_walk_length(oracle, gpu, feats, waves, launch_overrides):
     _check_windows(oracle, csr, fmt, y, pk, sc, windows, "walk lengths")
 
 
+@pytest.mark.parametrize("waves", ["1", "2"])
+@pytest.mark.parametrize("feats", [128, 256])
+def test_spmm_non_finite_scales(oracle, gpu, feats, waves, launch_overrides):
+    """Scales of +inf, -inf and NaN (a caller may pass any scales). Such a slot's panel takes the FP32
+    path, whose MFMA also multiplies the SW's absent entries (zeros) by the slot's non-finite
+    features, so NaN may spread over rows of that SW that do not reference the source; the
+    reference's tensor-core tiles do the same over their rows. Tiling-independent checks: every
+    element the oracle makes non-finite is non-finite here, every finite element here matches the
+    oracle, and SWs without such a source are all finite."""
+    launch_overrides(task_waves=int(waves))
+    csr = T.synth_csr("t2000_16_5")
+    fmt = T.convert_csr_to_sw32(csr.rows, csr.cols, csr)
+    x = features(csr.cols, feats, seed=9)
+    packed, scale, _, sc, pk = gpu_prepare(x, gpu)
+    bad = {3: float("inf"), 10: float("nan"), 20: float("-inf")}
+    for c, v in bad.items():
+        scale[c] = v
+        sc[c] = v
+    _, y = _run(fmt, packed, scale, feats, gpu)
+    y_ref = oracle.spmm_csr_f64(csr.rows, csr.row_offsets, csr.source_ids, csr.values, pk, sc, csr.cols)
+    assert np.isnan(y_ref).any() and np.isinf(y_ref).any()
+    assert not np.isfinite(y[~np.isfinite(y_ref)]).any()
+    fin = np.isfinite(y)
+    assert np.isfinite(y_ref[fin]).all()
+    assert_close(np.where(fin, y, 0.0), np.where(fin, y_ref, 0.0), "finite elements")
+    off = csr.row_offsets.astype(np.int64)
+    touched = np.zeros(csr.rows, bool)
+    for r in range(csr.rows):
+        touched[r] = np.isin(csr.source_ids[off[r]:off[r + 1]], list(bad)).any()
+    sw = np.arange(csr.rows) // 32
+    sw_has = np.zeros(sw[-1] + 1, bool)
+    np.logical_or.at(sw_has, sw, touched)
+    assert np.isfinite(y[~sw_has[sw]]).all()
+
+
 @pytest.mark.parametrize("feats", [128, 256])
 def test_spmm_huge_a_values_stay_finite(oracle, gpu, feats):
     """A values at and above 2^118 (where tf32(a) * 2^10 would overflow FP32) up to 3e38 and 2^127,
