@@ -1,7 +1,7 @@
 """Benchmark: ms per SpMM and achieved HBM GB/s of the fused INT8-dequant SpMM on one MI355X.
 
-Workload (BASELINE.json configs[2] / [3]): the synthetic 2,449,029-row / 126,167,053-nnz power-law
-matrix ("c3"), F128 (the line's `value`) and F256 (reported under "f256"). A "step" is one
+Workload: the synthetic 2,449,029-row / 126,167,053-nnz power-law matrix ("c3", the configuration the
+headline metric is quoted on), F128 (the line's `value`) and F256 (reported under "f256"). A "step" is one
 launchSpmmInt8 over the whole matrix with A, X, scales and the workspace already resident in HBM.
 Timing mirrors the reference harness (src/main.cu:30-51): W warm-up launches, synchronize, then
 HIP events (on the launch stream) around K launches; ms_per_step = elapsed / K.
